@@ -1,0 +1,134 @@
+"""ctypes binding of libakt_amd.so (the C ABI declared in include/akt_amd.h).
+
+The library is loaded after torch, so it binds to the HIP runtime torch has
+already loaded (both carry the soname libamdhip64.so.7).  There is no fallback
+path: if the library is missing, every entry point raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "libakt_amd.so"
+
+AKT_OK = 0
+_ERRORS = {1: "invalid argument", 2: "unsupported", 3: "workspace", 4: "HIP error"}
+
+_i64 = C.c_int64
+_p = C.c_void_p
+_i64x = C.POINTER(C.c_int64)
+
+# name -> (restype, argtypes)
+_SIGNATURES = {
+    "akt_last_error": (C.c_char_p, []),
+    "akt_abi_version": (C.c_int, []),
+    "akt_prefill_fwd": (C.c_int, [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64,
+                                  _i64x, _i64x, _i64x, _i64x, C.c_float, C.c_int, _p, C.c_int, _p]),
+    "akt_decode_workspace_size": (C.c_size_t, [_i64, _i64, _i64, _i64, _i64, _i64]),
+    "akt_decode_fwd": (C.c_int, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64,
+                                 _i64x, _i64x, _i64x, C.c_float, _i64, _p, C.c_size_t, _p]),
+    "akt_decode_paged_workspace_size": (C.c_size_t, [_i64, _i64, _i64, _i64, _i64, _i64, _i64]),
+    "akt_decode_paged_fwd": (C.c_int, [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64,
+                                       _i64, _i64, _i64x, _i64x, C.c_float, _i64, _p, C.c_size_t, _p]),
+    "akt_sparse_decode_workspace_size": (C.c_size_t, [_i64, _i64, _i64, _i64, _i64]),
+    "akt_sparse_decode_fwd": (C.c_int, [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64,
+                                        _i64, _i64x, _i64x, _i64x, _i64x, _i64x, C.c_float, _i64,
+                                        _p, C.c_size_t, _p]),
+    "akt_sparse_decode_paged_fwd": (C.c_int, [_p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64,
+                                              _i64, _i64, _i64, _i64, _i64x, _i64x, _i64x, _i64x,
+                                              C.c_float, _i64, _p, C.c_size_t, _p]),
+    "akt_magicpig_decode_paged_fwd": (C.c_int, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64,
+                                                _i64, _i64, _i64, _i64, _i64, _i64, _i64x, _i64x,
+                                                _i64x, _i64x, _i64, _p, C.c_size_t, _p]),
+    "akt_kept_index_from_mask": (C.c_int, [_p, _i64, _i64, _i64, _p, _p, _i64, _p, C.c_int, _p]),
+    "akt_kept_index_from_uniform": (C.c_int, [_p, C.c_float, _i64, _i64, _i64, _p, _p, _i64, _p,
+                                              C.c_int, _p]),
+    "akt_kernel_timer_enable": (C.c_int, [C.c_int]),
+    "akt_kernel_timer_read": (C.c_int, [C.POINTER(C.c_double), C.POINTER(C.c_int64)]),
+}
+
+_lib = None
+
+
+def library_path() -> Path:
+    return Path(os.environ.get("AKT_AMD_LIB", LIB_PATH))
+
+
+def load() -> C.CDLL:
+    """Load libakt_amd.so once and attach the C signatures."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    path = library_path()
+    if not path.exists():
+        raise RuntimeError(
+            f"{path} is not built: run `python -m attention_kernel_triton_amd.build` "
+            "(the HIP kernels have no fallback implementation)")
+    lib = C.CDLL(str(path))
+    for name, (res, args) in _SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def exported_symbols() -> list[str]:
+    return list(_SIGNATURES)
+
+
+def check(rc: int, what: str) -> None:
+    if rc != AKT_OK:
+        msg = load().akt_last_error().decode(errors="replace")
+        raise RuntimeError(f"{what} failed ({_ERRORS.get(rc, rc)}): {msg}")
+
+
+def strides(t: torch.Tensor, n: int | None = None):
+    s = list(t.stride())
+    if n is not None:
+        s = s[:n]
+    return (C.c_int64 * len(s))(*s)
+
+
+def i64s(*vals):
+    return (C.c_int64 * len(vals))(*vals)
+
+
+def ptr(t: torch.Tensor | None):
+    return None if t is None else C.c_void_p(t.data_ptr())
+
+
+def stream_of(t: torch.Tensor):
+    return C.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def workspace(nbytes: int, device) -> torch.Tensor | None:
+    if nbytes == 0:
+        return None
+    return torch.empty(int(nbytes), dtype=torch.uint8, device=device)
+
+
+class kernel_timer:
+    """Context manager: HIP-event time of each entry point's dominant kernel.
+
+    >>> with kernel_timer() as t:
+    ...     run()
+    >>> t.total_ms, t.launches
+    """
+
+    def __enter__(self):
+        check(load().akt_kernel_timer_enable(1), "akt_kernel_timer_enable")
+        self.total_ms, self.launches = 0.0, 0
+        return self
+
+    def __exit__(self, *exc):
+        lib = load()
+        ms, n = C.c_double(0.0), C.c_int64(0)
+        rc = lib.akt_kernel_timer_read(C.byref(ms), C.byref(n))
+        lib.akt_kernel_timer_enable(0)
+        check(rc, "akt_kernel_timer_read")
+        self.total_ms, self.launches = ms.value, n.value
+        return False

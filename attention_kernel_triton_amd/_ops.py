@@ -1,0 +1,263 @@
+"""Tensor-level wrappers over the C ABI (include/akt_amd.h).
+
+Each function validates devices, dtypes and layouts, allocates outputs and the
+split-KV workspace through torch's caching allocator, and launches on the
+current HIP stream of the input's device.  They never synchronise and never
+fall back to another implementation.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+from . import _native as N
+
+
+def _need_gpu(name: str, t: torch.Tensor) -> None:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor")
+    if t.device.type != "cuda":
+        raise ValueError(f"{name} must be on a ROCm GPU device, got {t.device}")
+
+
+def _half_rows(name: str, t: torch.Tensor) -> torch.Tensor:
+    """fp16 tensor with unit innermost stride and 16-byte aligned rows."""
+    _need_gpu(name, t)
+    if t.dtype != torch.float16:
+        raise TypeError(f"{name} must be float16, got {t.dtype}")
+    ok = t.stride(-1) == 1 and t.data_ptr() % 16 == 0 and all(
+        (s * 2) % 16 == 0 for s in t.stride()[:-1])
+    return t if ok else t.contiguous()
+
+
+def _int32(name: str, t: torch.Tensor, device) -> torch.Tensor:
+    _need_gpu(name, t)
+    if t.device != device:
+        raise ValueError(f"{name} is on {t.device}, expected {device}")
+    if t.dtype != torch.int32:
+        raise TypeError(f"{name} must be int32, got {t.dtype}")
+    return t
+
+
+def _same_device(dev, **tensors) -> None:
+    for name, t in tensors.items():
+        if t.device != dev:
+            raise ValueError(f"{name} is on {t.device}, expected {dev}")
+
+
+# --------------------------------------------------------------------------- prefill
+def prefill(Q, K, V, causal: bool, softmax_scale: float, varlen=None) -> torch.Tensor:
+    """O = softmax(scale * Q K^T [+ causal mask]) V for Q [B,Hq,S,D], K/V [B,Hkv,S,D]."""
+    Q = _half_rows("Q", Q)
+    K = _half_rows("K", K)
+    V = _half_rows("V", V)
+    _same_device(Q.device, K=K, V=V)
+    B, H, S, D = Q.shape
+    O = torch.empty((B, H, S, D), dtype=Q.dtype, device=Q.device)
+    vptr, vbits = None, 0
+    if varlen is not None:
+        _need_gpu("varlen", varlen)
+        if varlen.dtype not in (torch.int32, torch.int64):
+            raise TypeError(f"varlen must be int32 or int64, got {varlen.dtype}")
+        if varlen.numel() != B:
+            raise ValueError(f"varlen must have {B} entries, got {varlen.numel()}")
+        varlen = varlen.contiguous()
+        vptr, vbits = N.ptr(varlen), (64 if varlen.dtype == torch.int64 else 32)
+    lib = N.load()
+    rc = lib.akt_prefill_fwd(N.ptr(Q), N.ptr(K), N.ptr(V), N.ptr(O), B, H, K.shape[1], S, D,
+                             N.strides(Q), N.strides(K), N.strides(V), N.strides(O),
+                             float(softmax_scale), 1 if causal else 0, vptr, vbits,
+                             N.stream_of(Q))
+    N.check(rc, "akt_prefill_fwd")
+    return O
+
+
+# --------------------------------------------------------------------------- decode
+def decode(q, K, V, softmax_scale: float, return_lse: bool = False, chunk_tokens: int = 0):
+    """Single-query GQA decode: q [B,Hq,1,D], K/V [B,Hkv,S,D] -> o [B,Hq,1,D] (, lse [B,Hq])."""
+    q = _half_rows("q", q)
+    K = _half_rows("K", K)
+    V = _half_rows("V", V)
+    _same_device(q.device, K=K, V=V)
+    B, Hq, _, D = q.shape
+    Hkv, S = K.shape[1], K.shape[2]
+    o = torch.empty((B, Hq, 1, D), dtype=q.dtype, device=q.device)
+    lse = torch.empty((B, Hq), dtype=torch.float32, device=q.device) if return_lse else None
+    lib = N.load()
+    ws_n = lib.akt_decode_workspace_size(B, Hq, Hkv, S, D, chunk_tokens)
+    ws = N.workspace(ws_n, q.device)
+    rc = lib.akt_decode_fwd(N.ptr(q), N.ptr(K), N.ptr(V), N.ptr(o), N.ptr(lse), B, Hq, Hkv, S, D,
+                            N.strides(q), N.strides(K), N.strides(V), float(softmax_scale),
+                            chunk_tokens, N.ptr(ws), ws_n, N.stream_of(q))
+    N.check(rc, "akt_decode_fwd")
+    return (o, lse) if return_lse else o
+
+
+def decode_paged(q, paged_kv_cache, kv_page_indptr, kv_page_indices, kv_last_page_len,
+                 softmax_scale: float | None = None, return_lse: bool = False,
+                 chunk_tokens: int = 0):
+    """Paged decode: q [B,Hq,1,D] (or [B,Hq,D]), pool [P,2,Hkv,page,D] -> o [B,Hq,D]."""
+    q = _half_rows("q", q)
+    pool = _half_rows("paged_kv_cache", paged_kv_cache)
+    dev = q.device
+    _same_device(dev, paged_kv_cache=pool)
+    indptr = _int32("kv_page_indptr", kv_page_indptr, dev)
+    indices = _int32("kv_page_indices", kv_page_indices, dev)
+    last = _int32("kv_last_page_len", kv_last_page_len, dev)
+    indptr, indices, last = indptr.contiguous(), indices.contiguous(), last.contiguous()
+    B, Hq, D = q.shape[0], q.shape[1], q.shape[-1]
+    q4 = q if q.dim() == 4 else q.unsqueeze(2)
+    P, _, Hkv, page, Dc = pool.shape
+    if Dc != D:
+        raise ValueError(f"head_dim mismatch: q has {D}, cache has {Dc}")
+    if indptr.numel() != B + 1 or last.numel() != B:
+        raise ValueError("kv_page_indptr must have B+1 and kv_last_page_len B entries")
+    scale = float(1.0 / math.sqrt(D)) if softmax_scale is None else float(softmax_scale)
+    o = torch.empty((B, Hq, D), dtype=q.dtype, device=dev)
+    lse = torch.empty((B, Hq), dtype=torch.float32, device=dev) if return_lse else None
+    total = indices.numel()
+    lib = N.load()
+    ws_n = lib.akt_decode_paged_workspace_size(B, Hq, Hkv, D, page, total, chunk_tokens)
+    ws = N.workspace(ws_n, dev)
+    rc = lib.akt_decode_paged_fwd(N.ptr(q4), N.ptr(pool), N.ptr(indptr), N.ptr(indices),
+                                  N.ptr(last), N.ptr(o), N.ptr(lse), B, Hq, Hkv, D, page, total,
+                                  P, N.strides(q4), N.strides(pool), scale, chunk_tokens,
+                                  N.ptr(ws), ws_n, N.stream_of(q))
+    N.check(rc, "akt_decode_paged_fwd")
+    return (o, lse) if return_lse else o
+
+
+def _sparse_meta(sparse_ind, sparse_nnz, dev, B, Hq):
+    ind = _int32("sparse_ind", sparse_ind, dev)
+    nnz = _int32("sparse_nnz", sparse_nnz, dev)
+    if ind.dim() != 3 or ind.shape[0] != B or ind.shape[1] != Hq:
+        raise ValueError(f"sparse_ind must be [B={B}, H={Hq}, L_max], got {tuple(ind.shape)}")
+    if ind.stride(2) != 1:
+        ind = ind.contiguous()
+    if nnz.shape[0] != B or nnz.shape[1] != Hq or (nnz.dim() == 3 and nnz.shape[2] != 1):
+        raise ValueError(f"sparse_nnz must be [B={B}, H={Hq}(, 1)], got {tuple(nnz.shape)}")
+    return ind, nnz, N.i64s(ind.stride(0), ind.stride(1)), N.i64s(nnz.stride(0), nnz.stride(1))
+
+
+def sparse_decode(q, K, V, sparse_ind, sparse_nnz, softmax_scale: float,
+                  return_lse: bool = False, num_splits: int = 0):
+    """Sparse-token decode over dense K/V: returns o [B,Hq,1,D] (, lse [B,Hq])."""
+    q = _half_rows("q", q)
+    K = _half_rows("K", K)
+    V = _half_rows("V", V)
+    dev = q.device
+    _same_device(dev, K=K, V=V)
+    B, Hq, _, D = q.shape
+    Hkv, S = K.shape[1], K.shape[2]
+    ind, nnz, ist, nst = _sparse_meta(sparse_ind, sparse_nnz, dev, B, Hq)
+    L = ind.shape[2]
+    o = torch.empty((B, Hq, 1, D), dtype=q.dtype, device=dev)
+    lse = torch.empty((B, Hq), dtype=torch.float32, device=dev) if return_lse else None
+    lib = N.load()
+    ws_n = lib.akt_sparse_decode_workspace_size(B, Hq, D, L, num_splits)
+    ws = N.workspace(ws_n, dev)
+    rc = lib.akt_sparse_decode_fwd(N.ptr(q), N.ptr(K), N.ptr(V), N.ptr(ind), N.ptr(nnz),
+                                   N.ptr(o), N.ptr(lse), B, Hq, Hkv, S, D, L, N.strides(q),
+                                   N.strides(K), N.strides(V), ist, nst, float(softmax_scale),
+                                   num_splits, N.ptr(ws), ws_n, N.stream_of(q))
+    N.check(rc, "akt_sparse_decode_fwd")
+    return (o, lse) if return_lse else o
+
+
+def sparse_decode_paged(q, paged_kv_cache, kv_page_indptr, kv_page_indices, sparse_ind,
+                        sparse_nnz, softmax_scale: float | None = None, return_lse: bool = False,
+                        num_splits: int = 0, lsh_k=None, lsh_l=None):
+    """Sparse-token paged decode (plain, or MagicPIG when lsh_k/lsh_l are given)."""
+    q = _half_rows("q", q)
+    pool = _half_rows("paged_kv_cache", paged_kv_cache)
+    dev = q.device
+    _same_device(dev, paged_kv_cache=pool)
+    indptr = _int32("kv_page_indptr", kv_page_indptr, dev).contiguous()
+    indices = _int32("kv_page_indices", kv_page_indices, dev).contiguous()
+    B, Hq, D = q.shape[0], q.shape[1], q.shape[-1]
+    q4 = q if q.dim() == 4 else q.unsqueeze(2)
+    P, _, Hkv, page, Dc = pool.shape
+    if Dc != D:
+        raise ValueError(f"head_dim mismatch: q has {D}, cache has {Dc}")
+    if indptr.numel() != B + 1:
+        raise ValueError("kv_page_indptr must have B+1 entries")
+    ind, nnz, ist, nst = _sparse_meta(sparse_ind, sparse_nnz, dev, B, Hq)
+    L = ind.shape[2]
+    o = torch.empty((B, Hq, D), dtype=q.dtype, device=dev)
+    lse = torch.empty((B, Hq), dtype=torch.float32, device=dev) if return_lse else None
+    lib = N.load()
+    ws_n = lib.akt_sparse_decode_workspace_size(B, Hq, D, L, num_splits)
+    ws = N.workspace(ws_n, dev)
+    if lsh_k is None:
+        scale = float(1.0 / math.sqrt(D)) if softmax_scale is None else float(softmax_scale)
+        rc = lib.akt_sparse_decode_paged_fwd(N.ptr(q4), N.ptr(pool), N.ptr(indptr), N.ptr(indices),
+                                             N.ptr(ind), N.ptr(nnz), N.ptr(o), N.ptr(lse), B, Hq,
+                                             Hkv, D, page, P, L, N.strides(q4), N.strides(pool),
+                                             ist, nst, scale, num_splits, N.ptr(ws), ws_n,
+                                             N.stream_of(q))
+        N.check(rc, "akt_sparse_decode_paged_fwd")
+    else:
+        for name, t in (("K", lsh_k), ("L", lsh_l)):
+            _need_gpu(name, t)
+            if t.dtype != torch.float32 or tuple(t.shape) != (B, Hq):
+                raise ValueError(f"MagicPIG {name} must be float32 [{B}, {Hq}]")
+        lk, ll = lsh_k.contiguous(), lsh_l.contiguous()
+        rc = lib.akt_magicpig_decode_paged_fwd(N.ptr(q4), N.ptr(pool), N.ptr(indptr),
+                                               N.ptr(indices), N.ptr(ind), N.ptr(nnz), N.ptr(lk),
+                                               N.ptr(ll), N.ptr(o), N.ptr(lse), B, Hq, Hkv, D,
+                                               page, P, L, N.strides(q4), N.strides(pool), ist,
+                                               nst, num_splits, N.ptr(ws), ws_n, N.stream_of(q))
+        N.check(rc, "akt_magicpig_decode_paged_fwd")
+    return (o, lse) if return_lse else o
+
+
+# --------------------------------------------------------------------------- kept-index
+def kept_indices(l_max: int, mask=None, uniform=None, kept_ratio: float | None = None,
+                 row_len=None, ensure_nonempty: bool = True):
+    """Sorted kept-token index lists from a keep mask or uniform draws.
+
+    mask: bool/uint8 [..., N]; or uniform: float32 [..., N] with kept_ratio
+    (keep where uniform < kept_ratio).  row_len (int32 [...]) limits each row.
+    Returns (sparse_ind int32 [..., l_max] padded with -1, sparse_nnz int32 [..., 1]).
+    """
+    src = mask if mask is not None else uniform
+    if src is None or (mask is not None and uniform is not None):
+        raise ValueError("pass exactly one of mask= or uniform=")
+    _need_gpu("mask" if mask is not None else "uniform", src)
+    lead = tuple(src.shape[:-1])
+    n = src.shape[-1]
+    rows = 1
+    for s in lead:
+        rows *= s
+    dev = src.device
+    ind = torch.empty(lead + (int(l_max),), dtype=torch.int32, device=dev)
+    nnz = torch.empty(lead + (1,), dtype=torch.int32, device=dev)
+    rl = None
+    if row_len is not None:
+        rl = _int32("row_len", row_len, dev).contiguous()
+        if rl.numel() != rows:
+            raise ValueError("row_len must have one entry per row")
+    lib = N.load()
+    if mask is not None:
+        m = src.reshape(rows, n)
+        if m.dtype == torch.bool:
+            m = m.view(torch.uint8)
+        if m.dtype != torch.uint8:
+            raise TypeError("mask must be bool or uint8")
+        m = m.contiguous()
+        rc = lib.akt_kept_index_from_mask(N.ptr(m), rows, n, n, N.ptr(rl), N.ptr(ind), int(l_max),
+                                          N.ptr(nnz), 1 if ensure_nonempty else 0, N.stream_of(m))
+        N.check(rc, "akt_kept_index_from_mask")
+    else:
+        if kept_ratio is None:
+            raise ValueError("kept_ratio is required with uniform=")
+        u = src.reshape(rows, n)
+        if u.dtype != torch.float32:
+            raise TypeError("uniform must be float32")
+        u = u.contiguous()
+        rc = lib.akt_kept_index_from_uniform(N.ptr(u), float(kept_ratio), rows, n, n, N.ptr(rl),
+                                             N.ptr(ind), int(l_max), N.ptr(nnz),
+                                             1 if ensure_nonempty else 0, N.stream_of(u))
+        N.check(rc, "akt_kept_index_from_uniform")
+    return ind, nnz

@@ -1,0 +1,108 @@
+// Shared device helpers for the gfx950 attention kernels.
+//
+// Everything here is written for CDNA4 (gfx950): 64-lane wavefronts, MFMA
+// f16 shapes with the doubled K depth (16x16x32, 32x32x16), and the
+// v_permlane{16,32}_swap lane exchanges.  There is no other target.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace akt {
+
+typedef _Float16 half_t;
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+typedef float float16_t __attribute__((ext_vector_type(16)));
+typedef uint32_t uint4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kWave = 64;
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+// ---------------------------------------------------------------------------
+// MFMA wrappers.  Operand convention used by every kernel in this library:
+//   A[m][k]: lane = m + M * g, element e   (g = lane / M)
+//   B[k][n]: lane = n + N * g, element e
+// where the reduction index k is the same function k(g, e) for A and B, so a
+// kernel may assign any physical index (head dim, key slot) to (g, e) as long
+// as both operands use the same assignment.
+//   16x16 result: lane = n + 16 * (m / 4), register m % 4
+//   32x32 result: lane = n + 32 * ((m / 4) % 2), register (m % 4) + 4 * (m / 8)
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float4_t mfma16x16x32(half8_t a, half8_t b, float4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ float16_t mfma32x32x16(half8_t a, half8_t b, float16_t c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+// ---------------------------------------------------------------------------
+// Cross-lane helpers.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float shfl_xor_f(float v, int mask) {
+  return __shfl_xor(v, mask, kWave);
+}
+__device__ __forceinline__ float shfl_f(float v, int src) { return __shfl(v, src, kWave); }
+__device__ __forceinline__ uint32_t shfl_u(uint32_t v, int src) {
+  return (uint32_t)__shfl((int)v, src, kWave);
+}
+
+// Max / sum over the two 32-lane halves of the wave (lane l and l ^ 32).
+__device__ __forceinline__ float xor32_max(float v) {
+  return fmaxf(v, shfl_xor_f(v, 32));
+}
+__device__ __forceinline__ float xor32_sum(float v) { return v + shfl_xor_f(v, 32); }
+
+// Reduce across the four 16-lane rows (l ^ 16, l ^ 32).
+__device__ __forceinline__ float rows_max(float v) {
+  v = fmaxf(v, shfl_xor_f(v, 16));
+  return fmaxf(v, shfl_xor_f(v, 32));
+}
+__device__ __forceinline__ float rows_sum(float v) {
+  v += shfl_xor_f(v, 16);
+  return v + shfl_xor_f(v, 32);
+}
+
+// ---------------------------------------------------------------------------
+// Arithmetic helpers.
+// ---------------------------------------------------------------------------
+// Hardware base-2 exponential (v_exp_f32).  exp2(-inf) = 0.
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// fp32 pair -> packed fp16 pair (round to nearest even).
+__device__ __forceinline__ uint32_t pack_half2(float lo, float hi) {
+  half2_t h = {(half_t)lo, (half_t)hi};
+  return __builtin_bit_cast(uint32_t, h);
+}
+__device__ __forceinline__ half2_t as_half2(uint32_t u) { return __builtin_bit_cast(half2_t, u); }
+
+// c + a.x * b.x + a.y * b.y with fp32 accumulation (v_dot2_f32_f16).
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2(as_half2(a), as_half2(b), c, false);
+}
+
+// Pair up two fp16 words from two registers: lo16(a) | lo16(b) << 16.
+__device__ __forceinline__ uint32_t pair_lo(uint32_t a, uint32_t b) {
+  return __builtin_amdgcn_perm(b, a, 0x05040100u);
+}
+// hi16(a) | hi16(b) << 16.
+__device__ __forceinline__ uint32_t pair_hi(uint32_t a, uint32_t b) {
+  return __builtin_amdgcn_perm(b, a, 0x07060302u);
+}
+
+__device__ __forceinline__ half8_t as_half8(uint4_t u) { return __builtin_bit_cast(half8_t, u); }
+__device__ __forceinline__ uint4_t as_uint4(half8_t h) { return __builtin_bit_cast(uint4_t, h); }
+
+// 16-byte global load / store.
+__device__ __forceinline__ uint4_t ld16(const void* p) {
+  return *reinterpret_cast<const uint4_t*>(p);
+}
+__device__ __forceinline__ void st16(void* p, uint4_t v) { *reinterpret_cast<uint4_t*>(p) = v; }
+
+// Readfirstlane for 32-bit ints: moves a wave-uniform value into an SGPR.
+__device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+}  // namespace akt

@@ -1,0 +1,57 @@
+// Host-side helpers shared by the C-ABI entry points: per-thread error
+// message, argument checks and launch-status translation.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stdint.h>
+#include <stdio.h>
+
+#include "../../include/akt_amd.h"
+
+namespace akt {
+
+// Sets the calling thread's error message and returns `code`.
+int set_error(int code, const char* fmt, ...);
+// Clears the calling thread's error message.
+void clear_error();
+
+// Returns AKT_ERR_HIP with a message if the last launch on this thread failed.
+int check_launch(const char* what);
+
+// Records a HIP event pair around a kernel launch while the kernel timer is
+// enabled (akt_kernel_timer_enable); a no-op otherwise.
+class KernelTimer {
+ public:
+  explicit KernelTimer(void* stream);
+  ~KernelTimer();
+  KernelTimer(const KernelTimer&) = delete;
+  KernelTimer& operator=(const KernelTimer&) = delete;
+  void stop();
+
+ private:
+  void* stream_;
+  hipEvent_t start_ = nullptr, stop_ = nullptr;
+  bool armed_ = false;
+};
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// True when every row that starts at `base + i * strides[j]` (element strides,
+// fp16 elements) is 16-byte aligned.
+inline bool rows_aligned16(const void* base, const int64_t* strides, int n) {
+  if (!aligned16(base)) return false;
+  for (int i = 0; i < n; ++i)
+    if ((strides[i] * 2) % 16 != 0) return false;
+  return true;
+}
+
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+inline int64_t round_up(int64_t a, int64_t b) { return ceil_div(a, b) * b; }
+
+}  // namespace akt
+
+#define AKT_CHECK(cond, ...)                                         \
+  do {                                                               \
+    if (!(cond)) return ::akt::set_error(AKT_ERR_INVALID_ARGUMENT, __VA_ARGS__); \
+  } while (0)

@@ -1,0 +1,25 @@
+"""Drop-in for the reference module prefill_flash_attention.py.
+
+``flash_attention_prefill`` keeps the reference signature, asserts and output
+allocation (prefill_flash_attention.py:342-383); the work runs in the gfx950
+MFMA kernel ``akt_prefill_fwd`` (csrc/prefill.hip).  The reference's tile-size
+environment variables (VAR_Q_SEQ_BLK_SIZE, VAR_KV_SEQ_BLK_SIZE) are accepted
+and ignored: results never depend on them.
+"""
+from __future__ import annotations
+
+from . import _ops
+
+
+def flash_attention_prefill(Q, K, V, causal, softmax_scale, GQA_group_size=1):
+    """O = softmax(softmax_scale * Q K^T [+ causal mask]) V.
+
+    Q: [B, H, S, D]; K, V: [B, H // GQA_group_size, S, D]; fp16 on a ROCm GPU.
+    Query head h attends kv head h // GQA_group_size (prefill_flash_attention.py:185).
+    Returns O: [B, H, S, D] in Q's dtype.
+    """
+    B, H, S, D = Q.shape
+    assert K.shape == (B, H // GQA_group_size, S, D)
+    assert V.shape == (B, H // GQA_group_size, S, D)
+    assert D % 64 == 0, "HEAD_DIM must be a multiple of 64?"
+    return _ops.prefill(Q, K, V, causal, softmax_scale)

@@ -1,0 +1,214 @@
+/*
+ * akt_amd.h - C ABI of the gfx950 attention kernel library (libakt_amd.so).
+ *
+ * Every entry point takes plain device pointers, element strides and sizes,
+ * launches asynchronously on the given HIP stream (passed as void*; NULL is
+ * the default stream) and returns AKT_OK or an error code; on error
+ * akt_last_error() returns a message for the calling thread.  Nothing here
+ * synchronises the stream or allocates device memory: the split-KV decode
+ * entry points take a caller-owned workspace of the size reported by the
+ * matching *_workspace_size() function.
+ *
+ * Tensor element types: q/k/v/o and KV pools are IEEE fp16; page tables,
+ * kept-token indices and counts are int32; MagicPIG K/L and LSE are fp32.
+ * Strides are in elements.  The innermost (head_dim) stride must be 1 and
+ * every row must start 16-byte aligned.
+ *
+ * Reference interfaces replaced (KiritoHugh/attention_kernel_triton):
+ *   prefill_flash_attention.py:342                       flash_attention_prefill
+ *   prefill_flash_attention_var_len_padding.py:348       flash_attention_prefill(varlen=)
+ *   decode_flash_attention_redundant.py:233              flash_attention_decode
+ *   decode_flash_attention_redundant_var_len_paged.py:228  flash_attention_decode_paged
+ *   sparsetoken_decode_flash_attention_redundant.py:127  sparsetoken_flash_attention_decode
+ *   sparsetoken_decode_flash_attention_redundant_var_len_paged.py:170
+ *                                                        sparsetoken_flash_attention_decode_paged
+ *   magicpig_sparsetoken_decode_flash_attention_redundant_var_len_paged_with_norm.py:166
+ *                                                        magicpig_sparsetoken_flash_attention_decode_paged
+ *   sparsetoken_decode_flash_attention_redundant.py:283-295 (kept-index selection, harness code)
+ */
+#ifndef AKT_AMD_H
+#define AKT_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define AKT_OK 0
+#define AKT_ERR_INVALID_ARGUMENT 1 /* shape, stride, alignment or value check failed */
+#define AKT_ERR_UNSUPPORTED 2      /* a valid request this build has no kernel for   */
+#define AKT_ERR_WORKSPACE 3        /* workspace missing or smaller than required      */
+#define AKT_ERR_HIP 4              /* the HIP runtime reported an error at launch     */
+
+/* Message describing the last failure on the calling thread ("" if none). */
+const char* akt_last_error(void);
+
+/* ABI version of this header (bumped on any signature change). */
+int akt_abi_version(void);
+
+/*
+ * Causal / non-causal GQA prefill, O = softmax(scale * Q K^T [+ causal]) V.
+ * Replaces prefill_flash_attention.py:342 and, with varlen != NULL,
+ * prefill_flash_attention_var_len_padding.py:348.
+ *   q, o: [batch, num_q_heads, seq_len, head_dim]; k, v: [batch, num_kv_heads,
+ *   seq_len, head_dim]; q head h reads kv head h / (num_q_heads / num_kv_heads).
+ *   varlen: optional device array [batch] of valid lengths (int32 when
+ *   varlen_bits == 32, int64 when 64, ignored when varlen == NULL).  Query
+ *   blocks of 64 rows that start at or beyond a sequence's length are not
+ *   written (as in the reference); rows < length never read keys >= length
+ *   when causal.
+ *   head_dim: 64 or 128.
+ */
+int akt_prefill_fwd(const void* q, const void* k, const void* v, void* o,
+                    int64_t batch, int64_t num_q_heads, int64_t num_kv_heads,
+                    int64_t seq_len, int64_t head_dim,
+                    const int64_t q_stride[4], const int64_t k_stride[4],
+                    const int64_t v_stride[4], const int64_t o_stride[4],
+                    float softmax_scale, int causal,
+                    const void* varlen, int varlen_bits, void* stream);
+
+/*
+ * Single-token GQA decode over a dense cache.  Replaces
+ * decode_flash_attention_redundant.py:233.
+ *   q: [batch, num_q_heads, 1, head_dim] (strides q_stride[0], [1], -, [3]);
+ *   k, v: [batch, num_kv_heads, seq_len, head_dim];
+ *   o: contiguous [batch, num_q_heads, head_dim] fp16;
+ *   lse: optional contiguous [batch, num_q_heads] fp32 (natural log of the
+ *   softmax normaliser of the scaled scores).  head_dim: 64, 128 or 256.
+ *   chunk_tokens: split-KV chunk length (multiple of 64), 0 = automatic.
+ */
+size_t akt_decode_workspace_size(int64_t batch, int64_t num_q_heads, int64_t num_kv_heads,
+                                 int64_t seq_len, int64_t head_dim, int64_t chunk_tokens);
+int akt_decode_fwd(const void* q, const void* k, const void* v, void* o, float* lse,
+                   int64_t batch, int64_t num_q_heads, int64_t num_kv_heads,
+                   int64_t seq_len, int64_t head_dim,
+                   const int64_t q_stride[4], const int64_t k_stride[4],
+                   const int64_t v_stride[4], float softmax_scale, int64_t chunk_tokens,
+                   void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Paged var-len GQA decode.  Replaces
+ * decode_flash_attention_redundant_var_len_paged.py:228.
+ *   kv_cache: [num_pool_pages, 2, num_kv_heads, page_size, head_dim] (K at
+ *   [:,0], V at [:,1]) with strides kv_stride[5];
+ *   kv_page_indptr [batch+1], kv_page_indices [total_pages],
+ *   kv_last_page_len [batch]: int32 CSR page table.  Sequence b has
+ *   (indptr[b+1]-indptr[b]-1)*page_size + last_page_len[b] tokens (0 when it
+ *   has no pages; last_page_len is clamped to [0, page_size]).  Page ids
+ *   outside [0, num_pool_pages) are skipped.
+ *   o: contiguous [batch, num_q_heads, head_dim]; lse optional [batch, num_q_heads].
+ */
+size_t akt_decode_paged_workspace_size(int64_t batch, int64_t num_q_heads, int64_t num_kv_heads,
+                                       int64_t head_dim, int64_t page_size, int64_t total_pages,
+                                       int64_t chunk_tokens);
+int akt_decode_paged_fwd(const void* q, const void* kv_cache, const int32_t* kv_page_indptr,
+                         const int32_t* kv_page_indices, const int32_t* kv_last_page_len,
+                         void* o, float* lse, int64_t batch, int64_t num_q_heads,
+                         int64_t num_kv_heads, int64_t head_dim, int64_t page_size,
+                         int64_t total_pages, int64_t num_pool_pages,
+                         const int64_t q_stride[4], const int64_t kv_stride[5],
+                         float softmax_scale, int64_t chunk_tokens,
+                         void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Sparse-token decode over a dense cache.  Replaces
+ * sparsetoken_decode_flash_attention_redundant.py:127.
+ *   sparse_ind: [batch, num_q_heads, l_max] int32 kept token indices
+ *   (ascending in the reference harness; order does not matter here), entry
+ *   i is used when i < sparse_nnz[b, h] (nnz is clamped to [0, l_max]).
+ *   Indices outside [0, seq_len) are skipped.  A head with no kept tokens
+ *   produces o = 0 and lse = -inf.
+ *   ind_stride: strides of sparse_ind over (batch, head) (last stride 1);
+ *   nnz_stride: strides of sparse_nnz over (batch, head).
+ */
+size_t akt_sparse_decode_workspace_size(int64_t batch, int64_t num_q_heads, int64_t head_dim,
+                                        int64_t l_max, int64_t num_splits);
+int akt_sparse_decode_fwd(const void* q, const void* k, const void* v,
+                          const int32_t* sparse_ind, const int32_t* sparse_nnz,
+                          void* o, float* lse, int64_t batch, int64_t num_q_heads,
+                          int64_t num_kv_heads, int64_t seq_len, int64_t head_dim, int64_t l_max,
+                          const int64_t q_stride[4], const int64_t k_stride[4],
+                          const int64_t v_stride[4], const int64_t ind_stride[2],
+                          const int64_t nnz_stride[2], float softmax_scale, int64_t num_splits,
+                          void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Sparse-token decode over a paged var-len cache.  Replaces
+ * sparsetoken_decode_flash_attention_redundant_var_len_paged.py:170.
+ * Kept token t of sequence b lives in page
+ * kv_page_indices[kv_page_indptr[b] + t / page_size], slot t % page_size.
+ * Tokens whose logical page is outside the sequence's page list, or whose
+ * page id is outside [0, num_pool_pages), are skipped.
+ */
+int akt_sparse_decode_paged_fwd(const void* q, const void* kv_cache,
+                                const int32_t* kv_page_indptr, const int32_t* kv_page_indices,
+                                const int32_t* sparse_ind, const int32_t* sparse_nnz,
+                                void* o, float* lse, int64_t batch, int64_t num_q_heads,
+                                int64_t num_kv_heads, int64_t head_dim, int64_t page_size,
+                                int64_t num_pool_pages, int64_t l_max,
+                                const int64_t q_stride[4], const int64_t kv_stride[5],
+                                const int64_t ind_stride[2], const int64_t nnz_stride[2],
+                                float softmax_scale, int64_t num_splits,
+                                void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * MagicPIG "with norm" sparse paged decode.  Replaces
+ * magicpig_sparsetoken_decode_flash_attention_redundant_var_len_paged_with_norm.py:166.
+ * Score of kept token i: q.k_i / sqrt(head_dim) - ln(u_i) with
+ *   c = q.k_i / (|q| |k_i| + 1e-8) clamped to [-1+1e-7, 1-1e-7],
+ *   p = clamp(1 - acos(c)/pi, 0, 1), x = p^K,
+ *   u = max(1 - (1-x)^L - L x (1-x)^(L-1), 1e-10)  (evaluated in fp64),
+ * with per-(batch, q head) K, L: contiguous fp32 [batch, num_q_heads].
+ * Workspace size: akt_sparse_decode_workspace_size().
+ */
+int akt_magicpig_decode_paged_fwd(const void* q, const void* kv_cache,
+                                  const int32_t* kv_page_indptr, const int32_t* kv_page_indices,
+                                  const int32_t* sparse_ind, const int32_t* sparse_nnz,
+                                  const float* lsh_k, const float* lsh_l,
+                                  void* o, float* lse, int64_t batch, int64_t num_q_heads,
+                                  int64_t num_kv_heads, int64_t head_dim, int64_t page_size,
+                                  int64_t num_pool_pages, int64_t l_max,
+                                  const int64_t q_stride[4], const int64_t kv_stride[5],
+                                  const int64_t ind_stride[2], const int64_t nnz_stride[2],
+                                  int64_t num_splits, void* workspace, size_t workspace_bytes,
+                                  void* stream);
+
+/*
+ * Kept-token index selection (the reference harness step at
+ * sparsetoken_decode_flash_attention_redundant.py:283-295 and
+ * sparsetoken_decode_flash_attention_redundant_var_len_paged.py:341-353).
+ * For each of `rows` rows: kept = {j < n_r : keep(r, j)} in ascending order,
+ * where n_r = row_len[r] (or n when row_len == NULL) and keep(r, j) is
+ *   mask[r * mask_row_stride + j] != 0            (akt_kept_index_from_mask)
+ *   uniform[r * row_stride + j] < kept_ratio      (akt_kept_index_from_uniform)
+ * If ensure_nonempty and nothing is kept, index 0 is kept.
+ * Writes sparse_ind[r * l_max + i] = kept[i] for i < min(|kept|, l_max) and -1
+ * for the rest of the row, and sparse_nnz[r] = |kept|.
+ */
+int akt_kept_index_from_mask(const uint8_t* mask, int64_t rows, int64_t n,
+                             int64_t mask_row_stride, const int32_t* row_len,
+                             int32_t* sparse_ind, int64_t l_max, int32_t* sparse_nnz,
+                             int ensure_nonempty, void* stream);
+int akt_kept_index_from_uniform(const float* uniform, float kept_ratio, int64_t rows, int64_t n,
+                                int64_t row_stride, const int32_t* row_len,
+                                int32_t* sparse_ind, int64_t l_max, int32_t* sparse_nnz,
+                                int ensure_nonempty, void* stream);
+
+/*
+ * Kernel timer (diagnostics; no counterpart in the reference, which times
+ * whole Python calls with triton.testing.do_bench).  While enabled, every
+ * entry point above records a HIP event pair around its dominant kernel on
+ * the launch stream.  akt_kernel_timer_read() waits for the recorded events
+ * and returns the summed elapsed milliseconds and the number of launches;
+ * akt_kernel_timer_enable() discards what was recorded.
+ */
+int akt_kernel_timer_enable(int enable);
+int akt_kernel_timer_read(double* total_ms, int64_t* launches);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* AKT_AMD_H */

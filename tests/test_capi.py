@@ -1,0 +1,109 @@
+"""The C-ABI library loads, exports every declared symbol and validates arguments.
+
+No test here launches a kernel: argument checks return before any GPU call.
+"""
+import ctypes as C
+import re
+from pathlib import Path
+
+import pytest
+
+from attention_kernel_triton_amd import _native as N
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "akt_amd.h"
+
+
+def declared_symbols():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(akt_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_entry_points():
+    names = declared_symbols()
+    assert "akt_decode_paged_fwd" in names and "akt_prefill_fwd" in names
+    assert set(names) == set(N.exported_symbols())
+
+
+def test_library_exports_every_declared_symbol():
+    lib = N.load()
+    for name in declared_symbols():
+        assert hasattr(lib, name), name
+    assert lib.akt_abi_version() == 1
+
+
+def _i64(*v):
+    return (C.c_int64 * len(v))(*v)
+
+
+def test_prefill_rejects_unsupported_head_dim():
+    lib = N.load()
+    s = _i64(4 * 96, 96, 96, 1)
+    rc = lib.akt_prefill_fwd(None, None, None, None, 1, 4, 2, 4, 96, s, s, s, s, 0.1, 1, None, 0,
+                             None)
+    assert rc == 2 and b"head_dim" in lib.akt_last_error()
+
+
+def test_prefill_rejects_bad_gqa_and_strides():
+    lib = N.load()
+    s = _i64(64 * 64, 64, 64, 1)
+    rc = lib.akt_prefill_fwd(None, None, None, None, 1, 6, 4, 4, 64, s, s, s, s, 0.1, 1, None, 0,
+                             None)
+    assert rc == 1 and b"multiple" in lib.akt_last_error()
+    bad = _i64(64 * 64, 64, 64, 2)
+    rc = lib.akt_prefill_fwd(None, None, None, None, 1, 4, 4, 4, 64, bad, s, s, s, 0.1, 1, None,
+                             0, None)
+    assert rc == 1 and b"stride" in lib.akt_last_error()
+
+
+def test_decode_paged_requires_workspace():
+    lib = N.load()
+    need = lib.akt_decode_paged_workspace_size(4, 8, 2, 128, 16, 100, 0)
+    assert need > 0
+    qs = _i64(8 * 128, 128, 128, 1)
+    ks = _i64(2 * 2 * 16 * 128, 2 * 16 * 128, 16 * 128, 128, 1)
+    rc = lib.akt_decode_paged_fwd(C.c_void_p(16), C.c_void_p(16), None, None, None,
+                                  C.c_void_p(16), None, 4, 8, 2, 128, 16, 100, 100, qs, ks, 0.1,
+                                  0, None, 0, None)
+    assert rc == 3 and b"workspace" in lib.akt_last_error()
+
+
+def test_sparse_rejects_unaligned_rows():
+    lib = N.load()
+    qs = _i64(32 * 128, 128, 128, 1)
+    ks = _i64(8 * 100 * 128, 100 * 128, 128, 1)
+    rc = lib.akt_sparse_decode_fwd(C.c_void_p(8), C.c_void_p(16), C.c_void_p(16), None, None,
+                                   C.c_void_p(16), None, 1, 32, 8, 100, 128, 10, qs, ks, ks,
+                                   _i64(320, 10), _i64(32, 1), 0.1, 0, None, 0, None)
+    assert rc == 1 and b"aligned" in lib.akt_last_error()
+
+
+def test_workspace_sizes_scale_with_problem():
+    lib = N.load()
+    a = lib.akt_decode_paged_workspace_size(32, 32, 8, 128, 16, 8448, 0)
+    b = lib.akt_decode_paged_workspace_size(32, 32, 8, 128, 16, 2 * 8448, 0)
+    assert 0 < a <= b
+    assert lib.akt_decode_workspace_size(8, 64, 16, 1024, 64, 1024) == 0  # one chunk: no partials
+    assert lib.akt_sparse_decode_workspace_size(1, 32, 128, 3840, 1) == 0
+    assert lib.akt_sparse_decode_workspace_size(1, 32, 128, 3840, 8) == 32 * 8 * 132 * 4
+
+
+def test_kept_index_rejects_short_row_stride():
+    lib = N.load()
+    rc = lib.akt_kept_index_from_mask(C.c_void_p(16), 4, 100, 50, None, C.c_void_p(16), 10,
+                                      C.c_void_p(16), 1, None)
+    assert rc == 1
+
+
+def test_python_entry_points_validate_before_launch():
+    import torch
+    from attention_kernel_triton_amd import (decode_flash_attention_redundant as dec,
+                                             prefill_flash_attention as pre)
+    Q = torch.zeros(1, 4, 8, 64, dtype=torch.float16)
+    K = torch.zeros(1, 2, 8, 64, dtype=torch.float16)
+    with pytest.raises(AssertionError):
+        pre.flash_attention_prefill(Q, K[:, :1], K, True, 0.1, 2)  # reference shape assert
+    with pytest.raises(ValueError):
+        pre.flash_attention_prefill(Q, K, K, True, 0.1, 2)  # CPU tensors are not accepted
+    with pytest.raises(AssertionError):
+        dec.flash_attention_decode(Q[:, :, :2], K, K, 0.1, 2)

@@ -1,0 +1,161 @@
+"""GPU parity of dense decode (R3) and paged var-len decode (R4)."""
+import math
+
+import pytest
+import torch
+
+from attention_kernel_triton_amd import decode_flash_attention_redundant as dec
+from attention_kernel_triton_amd import decode_flash_attention_redundant_var_len_paged as pg
+from attention_kernel_triton_amd import _ops
+from attention_kernel_triton_amd import synthetic as syn
+from helpers import assert_close
+from oracle import naive
+
+pytestmark = pytest.mark.gpu
+
+
+def _dec_inputs(seed, B, Hkv, G, S, D):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(B, Hkv * G, 1, D, generator=g).half()
+    K = torch.randn(B, Hkv, S, D, generator=g).half()
+    V = torch.randn(B, Hkv, S, D, generator=g).half()
+    return q, K, V
+
+
+@pytest.mark.parametrize("D", [64, 128, 256])
+@pytest.mark.parametrize("G", [1, 2, 4, 8, 16])
+@pytest.mark.parametrize("S", [1, 37, 1000])
+def test_decode_shapes(dev, D, G, S):
+    B, Hkv = 2, 2
+    q, K, V = _dec_inputs(D + G + S, B, Hkv, G, S, D)
+    o, lse = dec.flash_attention_decode(q.to(dev), K.to(dev), V.to(dev), 1 / math.sqrt(D), G,
+                                        return_lse=True)
+    ro, rl = naive.decode(q, K, V, 1 / math.sqrt(D), G)
+    assert o.shape == (B, Hkv * G, 1, D)
+    assert_close(o, ro, what=f"decode D={D} G={G} S={S}")
+    assert_close(lse, rl, atol=1e-4, what="decode lse")
+
+
+@pytest.mark.parametrize("chunk", [64, 128, 192, 4096])
+def test_decode_chunking_does_not_change_results(dev, chunk):
+    q, K, V = _dec_inputs(3, 2, 4, 4, 777, 128)
+    o, lse = _ops.decode(q.to(dev), K.to(dev), V.to(dev), 0.09, return_lse=True,
+                         chunk_tokens=chunk)
+    ro, rl = naive.decode(q, K, V, 0.09, 4)
+    assert_close(o, ro, what=f"chunk {chunk}")
+    assert_close(lse, rl, atol=1e-4, what=f"chunk {chunk} lse")
+
+
+def test_decode_config2_full(dev):
+    c = syn.decode_config()
+    o = dec.flash_attention_decode(c.q.to(dev), c.K.to(dev), c.V.to(dev), c.scale, c.group)
+    ro, _ = naive.decode(c.q, c.K, c.V, c.scale, c.group)
+    print(f"config 2 max abs err {assert_close(o, ro, what='config 2'):.3e}")
+
+
+def test_decode_empty_cache_gives_zeros(dev):
+    q, K, V = _dec_inputs(4, 1, 2, 2, 0, 64)
+    o, lse = dec.flash_attention_decode(q.to(dev), K.to(dev), V.to(dev), 0.1, 2, return_lse=True)
+    assert torch.equal(o.cpu(), torch.zeros_like(o.cpu())) and torch.isinf(lse).all()
+
+
+# --------------------------------------------------------------------------- paged
+def _paged_call(p, dev, **kw):
+    return pg.flash_attention_decode_paged(p.q.to(dev), p.pool.to(dev), p.indptr.to(dev),
+                                           p.indices.to(dev), p.last_len.to(dev), **kw)
+
+
+def test_paged_reference_fixture(dev):
+    """Page table of decode_flash_attention_redundant_var_len_paged.py:349-353."""
+    g = torch.Generator().manual_seed(6)
+    pool = torch.randn(16, 2, 2, 64, 64, generator=g).half()
+    indptr = torch.tensor([0, 4, 5, 8], dtype=torch.int32)
+    indices = torch.tensor([0, 1, 3, 5, 2, 6, 7, 4], dtype=torch.int32)
+    last = torch.tensor([2, 22, 3], dtype=torch.int32)
+    q = torch.randn(3, 4, 1, 64, generator=g).half()
+    o, lse = pg.flash_attention_decode_paged(q.to(dev), pool.to(dev), indptr.to(dev),
+                                             indices.to(dev), last.to(dev), return_lse=True)
+    ro, rl = naive.naive_paged_attention(q, pool, indptr, indices, last)
+    assert o.shape == (3, 4, 64)
+    assert_close(o, ro, what="paged fixture")
+    assert_close(lse, rl, atol=1e-4, what="paged fixture lse")
+
+
+@pytest.mark.parametrize("page", [1, 8, 16, 48, 64])
+@pytest.mark.parametrize("D", [64, 128, 256])
+def test_paged_page_sizes(dev, page, D):
+    p = syn.paged_config(seed=page * 3 + D, B=5, Hq=8, Hkv=2, D=D, page=page, min_len=1,
+                         max_len=700, extra_pages=7)
+    o, lse = _paged_call(p, dev, return_lse=True)
+    ro, rl = naive.naive_paged_attention(p.q, p.pool, p.indptr, p.indices, p.last_len)
+    assert_close(o, ro, what=f"paged page={page} D={D}")
+    assert_close(lse, rl, atol=1e-4, what="paged lse")
+
+
+def test_paged_empty_sequences_and_clamped_last_len(dev):
+    g = torch.Generator().manual_seed(9)
+    pool = torch.randn(10, 2, 2, 16, 128, generator=g).half()
+    q = torch.randn(4, 8, 1, 128, generator=g).half()
+    indptr = torch.tensor([0, 0, 3, 3, 5], dtype=torch.int32)  # sequences 0 and 2 are empty
+    indices = torch.tensor([9, 2, 4, 0, 7], dtype=torch.int32)
+    last = torch.tensor([5, 40, 3, 0], dtype=torch.int32)       # 40 clamps to 16, 0 drops a page
+    o, lse = pg.flash_attention_decode_paged(q.to(dev), pool.to(dev), indptr.to(dev),
+                                             indices.to(dev), last.to(dev), return_lse=True)
+    ro, rl = naive.naive_paged_attention(q, pool, indptr, indices, last)
+    o, lse = o.cpu(), lse.cpu()
+    assert torch.equal(o[0], torch.zeros_like(o[0])) and torch.equal(o[2], torch.zeros_like(o[2]))
+    assert torch.isinf(lse[0]).all() and torch.isinf(lse[2]).all()
+    assert_close(o, ro, what="paged edge cases")
+
+
+def test_paged_single_token_sequences_are_exact(dev):
+    """A one-token sequence returns its V row bit for bit (p = 1, l = 1)."""
+    g = torch.Generator().manual_seed(10)
+    pool = torch.randn(40, 2, 4, 16, 128, generator=g).half()
+    B = 12
+    indptr = torch.arange(B + 1, dtype=torch.int32)
+    indices = torch.randperm(40, generator=g)[:B].to(torch.int32)
+    last = torch.ones(B, dtype=torch.int32)
+    q = torch.randn(B, 16, 1, 128, generator=g).half()
+    o = pg.flash_attention_decode_paged(q.to(dev), pool.to(dev), indptr.to(dev), indices.to(dev),
+                                        last.to(dev)).cpu()
+    for b in range(B):
+        for h in range(16):
+            assert torch.equal(o[b, h], pool[int(indices[b]), 1, h // 4, 0])
+
+
+def test_paged_config3_full(dev):
+    p = syn.paged_config()
+    o, lse = _paged_call(p, dev, return_lse=True)
+    ro, rl = naive.naive_paged_attention(p.q, p.pool, p.indptr, p.indices, p.last_len)
+    err = assert_close(o, ro, what="config 3")
+    assert_close(lse, rl, atol=1e-4, what="config 3 lse")
+    print(f"config 3 max abs err {err:.3e}")
+
+
+def test_paged_config3_page_relabelling_is_bit_exact(dev):
+    """Renaming physical pages (and moving their contents) must not change a single bit."""
+    p = syn.paged_config(B=8, min_len=256, max_len=4096)
+    P = p.pool.shape[0]
+    perm = torch.randperm(P, generator=torch.Generator().manual_seed(1))
+    pool2 = torch.empty_like(p.pool)
+    pool2[perm] = p.pool                      # page i moves to slot perm[i]
+    indices2 = perm[p.indices.long()].to(torch.int32)
+    a = _paged_call(p, dev)
+    b = pg.flash_attention_decode_paged(p.q.to(dev), pool2.to(dev), p.indptr.to(dev),
+                                        indices2.to(dev), p.last_len.to(dev))
+    assert torch.equal(a, b)
+
+
+def test_paged_invalid_page_ids_are_skipped(dev):
+    g = torch.Generator().manual_seed(12)
+    pool = torch.randn(6, 2, 1, 16, 64, generator=g).half()
+    q = torch.randn(1, 2, 1, 64, generator=g).half()
+    indptr = torch.tensor([0, 3], dtype=torch.int32)
+    good = torch.tensor([4, 1], dtype=torch.int32)
+    o = pg.flash_attention_decode_paged(q.to(dev), pool.to(dev), indptr.to(dev),
+                                        torch.tensor([4, 99, 1], dtype=torch.int32).to(dev),
+                                        torch.tensor([16], dtype=torch.int32).to(dev))
+    ro, _ = naive.naive_paged_attention(q, pool, torch.tensor([0, 2], dtype=torch.int32), good,
+                                        torch.tensor([16], dtype=torch.int32))
+    assert_close(o, ro, what="invalid page skipped")

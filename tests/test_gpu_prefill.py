@@ -1,0 +1,117 @@
+"""GPU parity of the prefill kernels (R1 dense causal / non-causal, R2 var-len)."""
+import math
+
+import pytest
+import torch
+
+from attention_kernel_triton_amd import prefill_flash_attention as pre
+from attention_kernel_triton_amd import prefill_flash_attention_var_len_padding as prevar
+from attention_kernel_triton_amd import synthetic as syn
+from helpers import ATOL, assert_close
+from oracle import naive
+
+pytestmark = pytest.mark.gpu
+
+
+def _qkv(seed, B, Hq, Hkv, S, D):
+    g = torch.Generator().manual_seed(seed)
+    mk = lambda *s: torch.randn(s, generator=g).half()  # noqa: E731
+    return mk(B, Hq, S, D), mk(B, Hkv, S, D), mk(B, Hkv, S, D)
+
+
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("S", [1, 17, 64, 130, 257])
+def test_prefill_small_shapes(dev, D, causal, S):
+    B, Hq, Hkv = 2, 4, 2
+    Q, K, V = _qkv(S * 7 + D, B, Hq, Hkv, S, D)
+    out = pre.flash_attention_prefill(Q.to(dev), K.to(dev), V.to(dev), causal, 1 / math.sqrt(D),
+                                      Hq // Hkv)
+    ref = naive.prefill(Q, K, V, causal, 1 / math.sqrt(D), Hq // Hkv)
+    assert out.shape == Q.shape and out.dtype == torch.float16
+    assert_close(out, ref, what=f"prefill D={D} causal={causal} S={S}")
+
+
+@pytest.mark.parametrize("G", [1, 8])
+def test_prefill_group_sizes_and_unmapped_xcd_layout(dev, G):
+    B, Hkv, S, D = 3, 1, 200, 64  # B*Hkv not a multiple of 8: linear block order
+    Q, K, V = _qkv(G, B, Hkv * G, Hkv, S, D)
+    out = pre.flash_attention_prefill(Q.to(dev), K.to(dev), V.to(dev), True, 0.125, G)
+    assert_close(out, naive.prefill(Q, K, V, True, 0.125, G), what=f"G={G}")
+
+
+def test_prefill_strided_inputs(dev):
+    B, Hq, Hkv, S, D = 2, 8, 4, 192, 128
+    g = torch.Generator().manual_seed(5)
+    # [B, S, H, D] storage viewed as [B, H, S, D]
+    Qs = torch.randn(B, S, Hq, D, generator=g).half()
+    Ks = torch.randn(B, S, Hkv, D, generator=g).half()
+    Vs = torch.randn(B, S, Hkv, D, generator=g).half()
+    Q, K, V = (t.to(dev).transpose(1, 2) for t in (Qs, Ks, Vs))
+    assert not Q.is_contiguous()
+    out = pre.flash_attention_prefill(Q, K, V, True, 0.1, 2)
+    ref = naive.prefill(Qs.transpose(1, 2), Ks.transpose(1, 2), Vs.transpose(1, 2), True, 0.1, 2)
+    assert_close(out, ref, what="strided")
+
+
+def test_prefill_config0_full(dev):
+    c = syn.prefill_config(0)
+    out = pre.flash_attention_prefill(c.Q.to(dev), c.K.to(dev), c.V.to(dev), True, c.scale, c.group)
+    ref = naive.prefill(c.Q, c.K, c.V, True, c.scale, c.group, dtype=torch.float32)
+    err = assert_close(out, ref, what="config 0")
+    print(f"config 0 max abs err {err:.3e}")
+
+
+def test_prefill_varlen_config1_full(dev):
+    c = syn.prefill_config(1)
+    out = prevar.flash_attention_prefill(c.Q.to(dev), c.K.to(dev), c.V.to(dev), True, c.scale,
+                                         c.group, varlen=c.varlen.to(dev))
+    ref = naive.prefill_varlen(c.Q, c.K, c.V, True, c.scale, c.group, c.varlen,
+                               dtype=torch.float32)
+    S = c.Q.shape[2]
+    valid = (torch.arange(S)[None, :] < c.varlen[:, None])[:, None, :, None].expand(c.Q.shape)
+    err = assert_close(out, ref, what="config 1 valid rows", mask=valid)
+    print(f"config 1 max abs err {err:.3e}")
+
+
+@pytest.mark.parametrize("bits", [32, 64])
+def test_prefill_varlen_nonfinite_padding_never_leaks(dev, bits):
+    B, Hq, Hkv, S, D = 4, 4, 2, 256, 64
+    Q, K, V = _qkv(11, B, Hq, Hkv, S, D)
+    lens = torch.tensor([256, 1, 100, 191])
+    for b, L in enumerate(lens.tolist()):
+        Q[b, :, L:] = float("nan")
+        K[b, :, L:] = float("inf")
+        V[b, :, L:] = float("nan")
+    dt = torch.int32 if bits == 32 else torch.int64
+    out = prevar.flash_attention_prefill(Q.to(dev), K.to(dev), V.to(dev), True, 0.125, 2,
+                                         varlen=lens.to(dev, dt)).cpu()
+    Qc, Kc, Vc = Q.clone(), K.clone(), V.clone()
+    for b, L in enumerate(lens.tolist()):
+        Qc[b, :, L:] = 0
+        Kc[b, :, L:] = 0
+        Vc[b, :, L:] = 0
+    ref = naive.prefill_varlen(Qc, Kc, Vc, True, 0.125, 2, lens)
+    valid = (torch.arange(S)[None, :] < lens[:, None])[:, None, :, None].expand(Q.shape)
+    assert torch.isfinite(out[valid]).all()
+    assert_close(out, ref, what="var-len padding", mask=valid)
+
+
+def test_prefill_varlen_noncausal_matches_reference_semantics(dev):
+    """Non-causal var-len attends all S keys, padding included (reference behaviour)."""
+    B, Hq, Hkv, S, D = 2, 2, 1, 130, 64
+    Q, K, V = _qkv(12, B, Hq, Hkv, S, D)
+    lens = torch.tensor([130, 70])
+    out = prevar.flash_attention_prefill(Q.to(dev), K.to(dev), V.to(dev), False, 0.125, 2,
+                                         varlen=lens.to(dev))
+    ref = naive.prefill_varlen(Q, K, V, False, 0.125, 2, lens)
+    valid = (torch.arange(S)[None, :] < lens[:, None])[:, None, :, None].expand(Q.shape)
+    assert_close(out, ref, what="non-causal var-len", mask=valid)
+
+
+def test_prefill_is_deterministic(dev):
+    c = syn.prefill_config(0, B=2, Hq=8, Hkv=2, S=512)
+    args = (c.Q.to(dev), c.K.to(dev), c.V.to(dev), True, c.scale, c.group)
+    a = pre.flash_attention_prefill(*args)
+    b = pre.flash_attention_prefill(*args)
+    assert torch.equal(a, b)
