@@ -105,10 +105,27 @@ def stream_of(t: torch.Tensor):
     return C.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
 
 
+_WS_CACHE: dict = {}
+
+
 def workspace(nbytes: int, device) -> torch.Tensor | None:
+    """Decode workspace for the current stream of ``device``.
+
+    The C ABI requires the workspace's 256-byte counter header to be zero
+    before first use (each call leaves it zero) and a workspace to be reused
+    only by calls ordered on one stream, so one zero-initialised buffer is
+    kept per (device, stream) and grown when a call needs more.
+    """
     if nbytes == 0:
         return None
-    return torch.empty(int(nbytes), dtype=torch.uint8, device=device)
+    dev = torch.device(device)
+    key = (dev.index, torch.cuda.current_stream(dev).cuda_stream)
+    buf = _WS_CACHE.get(key)
+    if buf is None or buf.numel() < nbytes:
+        size = max(int(nbytes), 2 * buf.numel() if buf is not None else 0)
+        buf = torch.zeros(size, dtype=torch.uint8, device=dev)
+        _WS_CACHE[key] = buf
+    return buf
 
 
 class kernel_timer:

@@ -28,6 +28,7 @@ COMMON_FLAGS = [
     "-fPIC",
     "-Wall",
     "-Wno-unused-function",
+    "-Wno-pass-failed",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
 

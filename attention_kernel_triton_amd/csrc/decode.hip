@@ -27,6 +27,8 @@
 // which makes the probability broadcast a within-row shuffle.
 #include <math.h>
 
+#include <atomic>
+
 #include "akt_common.hpp"
 #include "akt_host.hpp"
 
@@ -36,6 +38,14 @@ enum : int { kModeDense = 0, kModePaged = 1, kModeSparseDense = 2, kModeSparsePa
 
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / kWave;
+// Split-KV chunk lengths (tokens) of dense and paged caches: 2, 4 or 8
+// 16-token groups per wave.
+constexpr int kMaxChunk = 512;
+// Largest batch whose paged chunk table fits the persistent kernel's LDS.
+constexpr int kMaxTableB = 1024;
+constexpr int kMaxDevices = 64;
+// Workspace header holding the scheduling counters; zero between launches.
+constexpr size_t kCounterBytes = 256;
 #define AKT_NEG_INF (-__builtin_inff())
 
 struct SplitParams {
@@ -51,6 +61,7 @@ struct SplitParams {
   const float* lsh_l;
   half_t* o;      // [B, Hq, D] contiguous
   float* lse;     // [B, Hq] or null
+  int* counters;   // [2]: work tickets, exited workgroups (zero between launches)
   float* part_o;  // [parts, GT, D]
   float* part_ml; // [parts, GT, 4]: running max, fp16-P normaliser, fp32 normaliser, pad
   int64_t q_sb, q_sh;
@@ -141,7 +152,31 @@ __device__ void chunk_span(const SplitParams& p, int b, int& cs_out, int& nch_ou
 // ---------------------------------------------------------------------------
 // Split kernel.
 // ---------------------------------------------------------------------------
-template <int D, int GT, int MODE, bool ALIGNED, bool MAGIC>
+// Resolved work item: a chunk [t0, t1) of one unit (wave-uniform values).
+struct Item {
+  int b, kvh, hq0, nh, t0, t1, pstart, np, direct;
+  int64_t pidx;
+};
+
+// Everything needed to issue the loads of one item's groups.
+struct IssueCtx {
+  const half_t* kb;  // K base of the unit (dense: + batch/head offset; paged: + head offset)
+  const half_t* vb;
+  int64_t k_dummy, v_dummy;  // offsets of the unit's q row from kb / vb
+  const int* ind_row;        // sparse: kept-index row
+  int t1, g_begin, pstart, np;
+  int page_pref, slot_pref;  // aligned paged: page id / slot of this wave's k-th group (lane k)
+};
+
+// PERSIST: the grid is sized to the machine and each workgroup walks items
+// blockIdx.x, blockIdx.x + gridDim.x, ... (dense and paged caches).  For a
+// paged cache the per-sequence chunk prefix is built once per workgroup in
+// LDS, so resolving an item needs no global loads.  Each wave streams its
+// groups continuously across items: the last two groups of an item are
+// followed by the first two of the next, issued before the item's
+// workgroup merge, so the memory pipeline never drains between items.
+// Otherwise (sparse units) one workgroup handles the item named by blockIdx.
+template <int D, int GT, int MODE, bool ALIGNED, bool MAGIC, int GPW, bool PERSIST>
 __global__ __launch_bounds__(kThreads) void split_kernel(SplitParams p) {
   constexpr int KPL = D / 4;                 // K elements per lane per group
   constexpr int KS = D / 32;                 // MFMA k-steps (8 elements each)
@@ -152,185 +187,216 @@ __global__ __launch_bounds__(kThreads) void split_kernel(SplitParams p) {
   constexpr bool SPARSE = (MODE == kModeSparseDense || MODE == kModeSparsePaged);
   constexpr bool PAGED_ADDR = (MODE == kModePaged || MODE == kModeSparsePaged);
   static_assert(!SPARSE || GT == 1, "sparse units hold one query head");
+  static_assert(SPARSE == (GPW == 0), "sparse units have a dynamic group count");
+  static_assert(!SPARSE || !PERSIST, "sparse units are not persistent");
+  static_assert(GPW == 0 || GPW >= 2, "the cross-item pipeline needs two groups per wave");
+  constexpr bool TABLE = PERSIST && MODE == kModePaged;
 
   __shared__ float sm_o[kWaves][GT][D];
   __shared__ float sm_m[kWaves][GT];
   __shared__ float sm_l[kWaves][GT];
   __shared__ float sm_e[kWaves][GT];
+  // Paged persistent: chunk prefix, length and first page of every sequence.
+  __shared__ int sm_cs[TABLE ? kMaxTableB + 1 : 1];
+  __shared__ int sm_len[TABLE ? kMaxTableB : 1];
+  __shared__ int sm_ps[TABLE ? kMaxTableB : 1];
+  __shared__ int sm_wtot[kWaves];
+  __shared__ int sm_next;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = uniform(tid >> 6);  // wave-uniform: keeps group math in SGPRs
   const int R = lane >> 4;
   const int c16 = lane & 15;
+  const int Y = p.Hkv * p.n_hg;  // units per chunk index (dense / paged)
+  const uint32_t kOnes = 0x3c003c00u;  // half2(1, 1)
 
-  // ---- resolve the work item -------------------------------------------
-  int b = 0, kvh = 0, hq0 = 0, nh = 1, t0 = 0, t1 = 0, pstart = 0, np = 0;
-  int64_t pidx = 0;
-  bool direct = false;
-  const int* ind_row = nullptr;
-  if constexpr (MODE == kModeDense) {
-    const int nch = (p.S + p.chunk - 1) / p.chunk;
-    const int x = blockIdx.x;
-    b = x / nch;
-    const int c = x - b * nch;
-    const int y = blockIdx.y;
-    kvh = y / p.n_hg;
-    const int hg = y - kvh * p.n_hg;
-    hq0 = kvh * p.G + hg * GT;
-    nh = min(GT, p.G - hg * GT);
-    t0 = c * p.chunk;
-    t1 = min(p.S, t0 + p.chunk);
-    pidx = (int64_t)x * gridDim.y + y;
-    direct = (nch == 1);
-  } else if constexpr (MODE == kModePaged) {
-    int c, nch, len;
-    if (!locate_chunk(p, blockIdx.x, b, c, nch, len)) return;
-    const int y = blockIdx.y;
-    kvh = y / p.n_hg;
-    const int hg = y - kvh * p.n_hg;
-    hq0 = kvh * p.G + hg * GT;
-    nh = min(GT, p.G - hg * GT);
-    t0 = c * p.chunk;
-    t1 = min(len, t0 + p.chunk);
-    pidx = (int64_t)blockIdx.x * gridDim.y + y;
-    direct = (nch == 1);
-    pstart = p.indptr[b];
-    np = p.indptr[b + 1] - pstart;
-  } else {
-    const int x = blockIdx.x;
-    const int u = x / p.n_split;
-    const int c = x - u * p.n_split;
-    b = u / p.Hq;
-    hq0 = u - b * p.Hq;
-    kvh = hq0 / p.G;
-    nh = 1;
-    int n = p.sparse_nnz[(int64_t)b * p.nnz_sb + (int64_t)hq0 * p.nnz_sh];
-    n = min(max(n, 0), p.l_max);
-    // Split c covers [c*per, min(n, (c+1)*per)); per is a multiple of 64 so
-    // every split starts on a 16-token group and splits never share a group.
-    const int per = ((n + p.n_split - 1) / p.n_split + 63) & ~63;
-    t0 = c * per;
-    t1 = max(t0, min(n, t0 + per));
-    pidx = x;
-    direct = (p.n_split == 1);
-    ind_row = p.sparse_ind + (int64_t)b * p.ind_sb + (int64_t)hq0 * p.ind_sh;
-    if constexpr (MODE == kModeSparsePaged) {
-      pstart = p.indptr[b];
-      np = p.indptr[b + 1] - pstart;
+  // ---- work item resolution ----------------------------------------------
+  auto finish_item = [&](Item& w, int x, int y, int c, int nch, int len) {
+    w.kvh = y / p.n_hg;
+    const int hg = y - w.kvh * p.n_hg;
+    w.hq0 = w.kvh * p.G + hg * GT;
+    w.nh = min(GT, p.G - hg * GT);
+    w.t0 = c * p.chunk;
+    w.t1 = min(len, w.t0 + p.chunk);
+    w.pidx = (int64_t)x * Y + y;
+    w.direct = (nch == 1);
+  };
+  // Item i of the persistent order: chunk index x = i / Y, unit y = i % Y.
+  auto resolve_persistent = [&](int i) -> Item {
+    Item w = {};
+    const int x = i / Y;
+    const int y = i - x * Y;
+    if constexpr (MODE == kModeDense) {
+      const int nch = (p.S + p.chunk - 1) / p.chunk;
+      w.b = x / nch;
+      finish_item(w, x, y, x - w.b * nch, nch, p.S);
+    } else if constexpr (TABLE) {
+      int lo = 0, hi = p.B - 1;  // last sequence whose first chunk is <= x
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (sm_cs[mid] <= x) lo = mid;
+        else hi = mid - 1;
+      }
+      w.b = lo;
+      w.pstart = sm_ps[lo];
+      w.np = (sm_len[lo] + p.page_size - 1) / p.page_size;
+      finish_item(w, x, y, x - sm_cs[lo], sm_cs[lo + 1] - sm_cs[lo], sm_len[lo]);
     }
-  }
+    return w;
+  };
+  auto resolve_block = [&]() -> Item {
+    Item w = {};
+    if constexpr (MODE == kModePaged) {
+      int c, nch, len;
+      if (!locate_chunk(p, blockIdx.x, w.b, c, nch, len)) {
+        w.b = -1;
+        return w;
+      }
+      finish_item(w, blockIdx.x, blockIdx.y, c, nch, len);
+      w.pstart = p.indptr[w.b];
+      w.np = p.indptr[w.b + 1] - w.pstart;
+    } else if constexpr (SPARSE) {
+      const int x = blockIdx.x;
+      const int u = x / p.n_split;
+      const int c = x - u * p.n_split;
+      w.b = u / p.Hq;
+      w.hq0 = u - w.b * p.Hq;
+      w.kvh = w.hq0 / p.G;
+      w.nh = 1;
+      int n = p.sparse_nnz[(int64_t)w.b * p.nnz_sb + (int64_t)w.hq0 * p.nnz_sh];
+      n = min(max(n, 0), p.l_max);
+      // Split c covers [c*per, min(n, (c+1)*per)); per is a multiple of 64 so
+      // every split starts on a 16-token group and splits never share a group.
+      const int per = ((n + p.n_split - 1) / p.n_split + 63) & ~63;
+      w.t0 = c * per;
+      w.t1 = max(w.t0, min(n, w.t0 + per));
+      w.pidx = x;
+      w.direct = (p.n_split == 1);
+      if constexpr (MODE == kModeSparsePaged) {
+        w.pstart = p.indptr[w.b];
+        w.np = p.indptr[w.b + 1] - w.pstart;
+      }
+    }
+    return w;
+  };
+  // The work item is wave-uniform; say so, so that the group loop and all
+  // per-group address math stay scalar.
+  auto make_uniform = [&](Item& w) {
+    w.b = uniform(w.b);
+    w.kvh = uniform(w.kvh);
+    w.hq0 = uniform(w.hq0);
+    w.nh = uniform(w.nh);
+    w.t0 = uniform(w.t0);
+    w.t1 = uniform(w.t1);
+    w.pstart = uniform(w.pstart);
+    w.np = uniform(w.np);
+    w.direct = uniform(w.direct);
+  };
 
-  const int64_t k_unit = PAGED_ADDR ? (int64_t)kvh * p.k_head
-                                    : (int64_t)b * p.k_batch + (int64_t)kvh * p.k_head;
-  const int64_t v_unit = PAGED_ADDR ? (int64_t)kvh * p.v_head
-                                    : (int64_t)b * p.v_batch + (int64_t)kvh * p.v_head;
-  const half_t* __restrict__ kb = p.kbase + k_unit;
-  const half_t* __restrict__ vb = p.vbase + v_unit;
-
-  // ---- query fragment (B operand): head hq0 + c16, dims R*KPL + 8s + e --
-  half8_t qf[KS];
-  {
-    const bool hv = c16 < nh;
-    const half_t* qrow = p.q + (int64_t)b * p.q_sb + (int64_t)(hq0 + (hv ? c16 : 0)) * p.q_sh + R * KPL;
+  // ---- per-item setup: issue context (with page prefetch) and q fragment ----
+  // Query fragment (B operand): head hq0 + c16, dims R*KPL + 8s + e.  For paged
+  // caches with page_size % 16 == 0 (one page per 16-token group), lane k
+  // prefetches the page id and slot of this wave's k-th group (a chunk has at
+  // most kMaxChunk tokens, so at most 8 groups per wave).
+  auto setup = [&](const Item& w, IssueCtx& cx, half8_t (&qd)[KS]) {
+    const int64_t k_unit = PAGED_ADDR ? (int64_t)w.kvh * p.k_head
+                                      : (int64_t)w.b * p.k_batch + (int64_t)w.kvh * p.k_head;
+    const int64_t v_unit = PAGED_ADDR ? (int64_t)w.kvh * p.v_head
+                                      : (int64_t)w.b * p.v_batch + (int64_t)w.kvh * p.v_head;
+    cx.kb = p.kbase + k_unit;
+    cx.vb = p.vbase + v_unit;
+    const half_t* qrow0 = p.q + (int64_t)w.b * p.q_sb + (int64_t)w.hq0 * p.q_sh;
+    cx.k_dummy = qrow0 - cx.kb;
+    cx.v_dummy = qrow0 - cx.vb;
+    cx.ind_row = nullptr;
+    if constexpr (SPARSE)
+      cx.ind_row = p.sparse_ind + (int64_t)w.b * p.ind_sb + (int64_t)w.hq0 * p.ind_sh;
+    cx.t1 = w.t1;
+    cx.g_begin = w.t0 >> 4;
+    cx.pstart = w.pstart;
+    cx.np = w.np;
+    cx.page_pref = 0;
+    cx.slot_pref = 0;
+    if constexpr (MODE == kModePaged && ALIGNED) {
+      const int g_end = (w.t1 + 15) >> 4;
+      const int gk = cx.g_begin + wave + kWaves * lane;
+      const int gc = min(gk, g_end - 1);  // clamped: the load is issued unconditionally
+      const int lp = (gc << 4) / p.page_size;
+      cx.page_pref = p.indices[w.pstart + lp];
+      cx.slot_pref = (gc << 4) - lp * p.page_size;
+    }
+    const bool hv = c16 < w.nh;
+    const half_t* qrow = qrow0 + (int64_t)(hv ? c16 : 0) * p.q_sh + R * KPL;
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
       uint4_t v = ld16(qrow + 8 * s);
       if (!hv) v = uint4_t{0, 0, 0, 0};
-      qf[s] = as_half8(v);
+      qd[s] = as_half8(v);
     }
-  }
+  };
 
-  // MagicPIG: |q|^2 for the unit's head (valid in lanes with c16 == 0).
-  float q_norm = 0.f;
-  float lsh_k = 0.f, lsh_l = 0.f;
-  if constexpr (MAGIC) {
-    float qs = 0.f;
-#pragma unroll
-    for (int s = 0; s < KS; ++s) {
-      uint4_t u = as_uint4(qf[s]);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) qs = dot2(u[j], u[j], qs);
-    }
-    q_norm = sqrtf(rows_sum(qs));
-    lsh_k = p.lsh_k[(int64_t)b * p.Hq + hq0];
-    lsh_l = p.lsh_l[(int64_t)b * p.Hq + hq0];
-  }
+  // One 16-token group in flight: its K slice, V rows and usable-token mask.
+  struct Buf {
+    uint4_t k[KS];
+    uint4_t v[VTOK][VLD];
+    uint32_t vmask;
+  };
 
-  float m_run = AKT_NEG_INF;  // running max of head c16 (log2 units)
-  // Partial normalisers over this lane's tokens: l_part sums the fp16-rounded
-  // probabilities that multiply V (so O is normalised consistently), e_part
-  // the fp32 probabilities (for the log-sum-exp output).
-  float l_part = 0.f;
-  float e_part = 0.f;
-  float acc[GT][VDIM];
-#pragma unroll
-  for (int h = 0; h < GT; ++h)
-#pragma unroll
-    for (int d = 0; d < VDIM; ++d) acc[h][d] = 0.f;
-
-  const uint32_t kOnes = 0x3c003c00u;  // half2(1, 1)
-  const int g_begin = t0 >> 4;
-  const int g_end = (t1 + 15) >> 4;
-
-  for (int g = g_begin + wave; g < g_end; g += kWaves) {
+  // Computes the row addresses of group g and issues its K/V loads.  Every
+  // load is issued unconditionally (a lane whose token is unusable reads the
+  // unit's own q row instead, which is always mapped and finite) so that no
+  // load sits behind a branch: the wait counts then only cover the buffer
+  // being consumed.  Index and page lookups read clamped, in-range entries.
+  auto issue = [&](const IssueCtx& cx, int g, Buf& bf) {
+    const int t1 = cx.t1;
     const int gpos = g << 4;
-
-    // ---- K lane: row of token gpos + c16 --------------------------------
     const int pos_k = gpos + c16;
-    int ra = 0, rb = 0, gpage = 0;
+    int ra = 0, rb = 0, gpage = 0, gslot = 0;
     bool kval = pos_k < t1;
     if constexpr (MODE == kModeDense) {
       ra = pos_k;
     } else if constexpr (MODE == kModePaged) {
       if constexpr (ALIGNED) {
-        const int lp = uniform(gpos / p.page_size);
-        const int page = p.indices[pstart + lp];
+        const int k = (g - cx.g_begin - wave) >> 2;
+        const int page = __builtin_amdgcn_readlane(cx.page_pref, k);
+        gslot = __builtin_amdgcn_readlane(cx.slot_pref, k);
         const bool page_ok = page >= 0 && page < p.num_pool_pages;
         kval = kval && page_ok;
         gpage = page_ok ? page : 0;
-        ra = page;
-        rb = gpos - lp * p.page_size + c16;
+        ra = gpage;
+        rb = gslot + c16;
       } else {
-        if (kval) {
-          const int lp = pos_k / p.page_size;
-          const int page = p.indices[pstart + lp];
-          kval = page >= 0 && page < p.num_pool_pages;
-          ra = page;
-          rb = pos_k - lp * p.page_size;
-        }
+        const int pc = min(pos_k, t1 - 1);  // t1 <= len, so pc's page is in the table
+        const int lp = pc / p.page_size;
+        const int page = p.indices[cx.pstart + lp];
+        kval = kval && page >= 0 && page < p.num_pool_pages;
+        ra = page;
+        rb = pc - lp * p.page_size;
       }
     } else if constexpr (MODE == kModeSparseDense) {
-      if (kval) {
-        const int t = ind_row[pos_k];
-        kval = t >= 0 && t < p.S;
-        ra = t;
-      }
+      const int t = cx.ind_row[min(pos_k, t1 - 1)];
+      kval = kval && t >= 0 && t < p.S;
+      ra = t;
     } else {  // sparse paged
-      if (kval) {
-        const int t = ind_row[pos_k];
-        const int lp = t >= 0 ? t / p.page_size : -1;
-        kval = t >= 0 && lp < np;
-        if (kval) {
-          const int page = p.indices[pstart + lp];
-          kval = page >= 0 && page < p.num_pool_pages;
-          ra = page;
-          rb = t - lp * p.page_size;
-        }
-      }
+      const int t = cx.ind_row[min(pos_k, t1 - 1)];
+      const int lp = t >= 0 ? t / p.page_size : 0;
+      kval = kval && t >= 0 && lp < cx.np;
+      // np == 0 (no pages) reads the nnz entry instead of an empty page table.
+      const int* pptr = cx.np > 0 ? p.indices + cx.pstart + min(lp, cx.np - 1) : p.sparse_nnz;
+      const int page = *pptr;
+      kval = kval && page >= 0 && page < p.num_pool_pages;
+      ra = page;
+      rb = t - lp * p.page_size;
     }
-    if (!kval) { ra = 0; rb = 0; }
-    const uint64_t vmask = __ballot(kval);  // bit t (< 16): token gpos + t usable
-
-    uint4_t kreg[KS];
+    const uint32_t vmask = (uint32_t)__ballot(kval) & 0xffffu;  // bit t: token gpos + t usable
+    bf.vmask = vmask;
     {
-      const half_t* kr = kb + (int64_t)ra * p.k_sa + (int64_t)rb * p.k_sb + R * KPL;
+      const int64_t off = (int64_t)ra * p.k_sa + (int64_t)rb * p.k_sb;
+      const half_t* kr = cx.kb + (kval ? off : cx.k_dummy) + R * KPL;
 #pragma unroll
-      for (int s = 0; s < KS; ++s) kreg[s] = kval ? ld16(kr + 8 * s) : uint4_t{0, 0, 0, 0};
+      for (int s = 0; s < KS; ++s) bf.k[s] = ld16(kr + 8 * s);
     }
-
-    // ---- V lane: tokens of this row ------------------------------------
-    uint4_t vreg[VTOK][VLD];
 #pragma unroll
     for (int i = 0; i < VTOK; ++i) {
       const int tt = (D == 64) ? (4 * R + 2 * (c16 >> 3) + i) : (4 * R + i);
@@ -341,21 +407,59 @@ __global__ __launch_bounds__(kThreads) void split_kernel(SplitParams p) {
         vbb = 0;
       } else if constexpr (MODE == kModePaged && ALIGNED) {
         va = gpage;  // the page is uniform over the group
-        vbb = gpos - (gpos / p.page_size) * p.page_size + tt;
+        vbb = gslot + tt;
       } else {
         va = __shfl(ra, tt, 64);
         vbb = __shfl(rb, tt, 64);
       }
       const int dim0 = (D == 64) ? 8 * (c16 & 7) : VDIM * c16;
-      const half_t* vr = vb + (int64_t)va * p.v_sa + (int64_t)vbb * p.v_sb + dim0;
+      const int64_t off = (int64_t)va * p.v_sa + (int64_t)vbb * p.v_sb;
+      const half_t* vr = cx.vb + (vv ? off : cx.v_dummy) + dim0;
 #pragma unroll
-      for (int j = 0; j < VLD; ++j) vreg[i][j] = vv ? ld16(vr + 8 * j) : uint4_t{0, 0, 0, 0};
+      for (int j = 0; j < VLD; ++j) bf.v[i][j] = ld16(vr + 8 * j);
     }
+  };
 
-    // ---- scores ----------------------------------------------------------
+  // ---- per-item accumulation state ----------------------------------------
+  Item it;
+  half8_t qf[KS];
+  float q_norm = 0.f, lsh_k = 0.f, lsh_l = 0.f;  // MagicPIG
+  float m_run;   // running max of head c16 (log2 units)
+  // Partial normalisers over this lane's tokens: l_part sums the fp16-rounded
+  // probabilities that multiply V (so O is normalised consistently), e_part
+  // the fp32 probabilities (for the log-sum-exp output).
+  float l_part, e_part;
+  float acc[GT][VDIM];
+
+  auto begin_item = [&]() {
+    m_run = AKT_NEG_INF;
+    l_part = 0.f;
+    e_part = 0.f;
+#pragma unroll
+    for (int h = 0; h < GT; ++h)
+#pragma unroll
+      for (int d = 0; d < VDIM; ++d) acc[h][d] = 0.f;
+    if constexpr (MAGIC) {
+      // |q|^2 of the unit's head (valid in lanes with c16 == 0).
+      float qs = 0.f;
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        uint4_t u = as_uint4(qf[s]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) qs = dot2(u[j], u[j], qs);
+      }
+      q_norm = sqrtf(rows_sum(qs));
+      lsh_k = p.lsh_k[(int64_t)it.b * p.Hq + it.hq0];
+      lsh_l = p.lsh_l[(int64_t)it.b * p.Hq + it.hq0];
+    }
+  };
+
+  // Scores, online softmax and P.V for a loaded group of the current item.
+  auto consume = [&](const Buf& bf) {
+    const uint32_t vmask = bf.vmask;
     float4_t sacc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int s = 0; s < KS; ++s) sacc = mfma16x16x32(as_half8(kreg[s]), qf[s], sacc);
+    for (int s = 0; s < KS; ++s) sacc = mfma16x16x32(as_half8(bf.k[s]), qf[s], sacc);
 
     float t[4];
     if constexpr (MAGIC) {
@@ -364,7 +468,7 @@ __global__ __launch_bounds__(kThreads) void split_kernel(SplitParams p) {
 #pragma unroll
       for (int s = 0; s < KS; ++s)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) ks = dot2(kreg[s][j], kreg[s][j], ks);
+        for (int j = 0; j < 4; ++j) ks = dot2(bf.k[s][j], bf.k[s][j], ks);
       ks = rows_sum(ks);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
@@ -389,7 +493,7 @@ __global__ __launch_bounds__(kThreads) void split_kernel(SplitParams p) {
         t[r] = ((vmask >> (4 * R + r)) & 1) ? sacc[r] * p.qk_scale : AKT_NEG_INF;
     }
 
-    // ---- online softmax (head c16) -------------------------------------
+    // online softmax (head c16)
     float mt = fmaxf(fmaxf(t[0], t[1]), fmaxf(t[2], t[3]));
     mt = rows_max(mt);
     const float m_new = fmaxf(m_run, mt);
@@ -414,7 +518,7 @@ __global__ __launch_bounds__(kThreads) void split_kernel(SplitParams p) {
     l_part = dot2(p23, kOnes, dot2(p01, kOnes, l_part));
     e_part += (pr[0] + pr[1]) + (pr[2] + pr[3]);
 
-    // ---- P.V -------------------------------------------------------------
+    // P.V
     uint32_t vp[NPAIR][VDIM];
 #pragma unroll
     for (int q2 = 0; q2 < NPAIR; ++q2)
@@ -422,7 +526,7 @@ __global__ __launch_bounds__(kThreads) void split_kernel(SplitParams p) {
       for (int j = 0; j < VLD; ++j)
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
-          const uint32_t a = vreg[2 * q2][j][w], bq = vreg[2 * q2 + 1][j][w];
+          const uint32_t a = bf.v[2 * q2][j][w], bq = bf.v[2 * q2 + 1][j][w];
           vp[q2][8 * j + 2 * w] = pair_lo(a, bq);
           vp[q2][8 * j + 2 * w + 1] = pair_hi(a, bq);
         }
@@ -440,68 +544,208 @@ __global__ __launch_bounds__(kThreads) void split_kernel(SplitParams p) {
         for (int d = 0; d < VDIM; ++d) acc[h][d] = dot2(pp, vp[q2][d], acc[h][d]);
       }
     }
-  }
+  };
 
-  // ---- wave reduction --------------------------------------------------
-  const float l_wave = rows_sum(l_part);
-  const float e_wave = rows_sum(e_part);
+  // Wave reduction, workgroup merge and output of the current item.
+  auto finish = [&]() {
+    const float l_wave = rows_sum(l_part);
+    const float e_wave = rows_sum(e_part);
 #pragma unroll
-  for (int h = 0; h < GT; ++h)
+    for (int h = 0; h < GT; ++h)
 #pragma unroll
-    for (int d = 0; d < VDIM; ++d) {
-      float v = acc[h][d];
-      if constexpr (D == 64) v += shfl_xor_f(v, 8);
-      acc[h][d] = rows_sum(v);
-    }
-  if (R == 0) {
-    const bool owner = (D == 64) ? (c16 < 8) : true;
-    if (owner) {
-      const int dim0 = (D == 64) ? 8 * c16 : VDIM * c16;
+      for (int d = 0; d < VDIM; ++d) {
+        float v = acc[h][d];
+        if constexpr (D == 64) v += shfl_xor_f(v, 8);
+        acc[h][d] = rows_sum(v);
+      }
+    if (R == 0) {
+      const bool owner = (D == 64) ? (c16 < 8) : true;
+      if (owner) {
+        const int dim0 = (D == 64) ? 8 * c16 : VDIM * c16;
 #pragma unroll
-      for (int h = 0; h < GT; ++h)
+        for (int h = 0; h < GT; ++h)
 #pragma unroll
-        for (int d = 0; d < VDIM; ++d) sm_o[wave][h][dim0 + d] = acc[h][d];
-    }
-    if (c16 < GT) {
-      sm_m[wave][c16] = m_run;
-      sm_l[wave][c16] = l_wave;
-      sm_e[wave][c16] = e_wave;
-    }
-  }
-  __syncthreads();
-
-  // ---- workgroup merge + output ----------------------------------------
-  for (int idx = tid; idx < GT * D; idx += kThreads) {
-    const int h = idx / D;
-    const int d = idx - h * D;
-    float M = AKT_NEG_INF;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, sm_m[w][h]);
-    float L = 0.f, E = 0.f, O = 0.f;
-    if (M != AKT_NEG_INF) {
-#pragma unroll
-      for (int w = 0; w < kWaves; ++w) {
-        const float f = fast_exp2(sm_m[w][h] - M);
-        L += f * sm_l[w][h];
-        E += f * sm_e[w][h];
-        O += f * sm_o[w][h][d];
+          for (int d = 0; d < VDIM; ++d) sm_o[wave][h][dim0 + d] = acc[h][d];
+      }
+      if (c16 < GT) {
+        sm_m[wave][c16] = m_run;
+        sm_l[wave][c16] = l_wave;
+        sm_e[wave][c16] = e_wave;
       }
     }
-    if (h >= nh) continue;
-    if (direct) {
-      const int64_t row = (int64_t)b * p.Hq + hq0 + h;
-      p.o[row * D + d] = (half_t)(L > 0.f ? O / L : 0.f);
-      if (d == 0 && p.lse) p.lse[row] = E > 0.f ? (M + log2f(E)) * kLn2 : AKT_NEG_INF;
+    __syncthreads();
+    const int b = it.b, hq0 = it.hq0, nh = it.nh;
+    const int64_t pidx = it.pidx;
+    for (int idx = tid; idx < GT * D; idx += kThreads) {
+      const int h = idx / D;
+      const int d = idx - h * D;
+      float M = AKT_NEG_INF;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) M = fmaxf(M, sm_m[w][h]);
+      float L = 0.f, E = 0.f, O = 0.f;
+      if (M != AKT_NEG_INF) {
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+          const float f = fast_exp2(sm_m[w][h] - M);
+          L += f * sm_l[w][h];
+          E += f * sm_e[w][h];
+          O += f * sm_o[w][h][d];
+        }
+      }
+      if (h >= nh) continue;
+      if (it.direct) {
+        const int64_t row = (int64_t)b * p.Hq + hq0 + h;
+        p.o[row * D + d] = (half_t)(L > 0.f ? O / L : 0.f);
+        if (d == 0 && p.lse) p.lse[row] = E > 0.f ? (M + log2f(E)) * kLn2 : AKT_NEG_INF;
+      } else {
+        p.part_o[(pidx * GT + h) * D + d] = O;
+        if (d == 0) {
+          float* ml = p.part_ml + (pidx * GT + h) * 4;
+          ml[0] = M;
+          ml[1] = L;
+          ml[2] = E;
+          ml[3] = 0.f;
+        }
+      }
+    }
+    __syncthreads();  // the merge buffers are reused by the next item
+  };
+
+  // ---- drivers ---------------------------------------------------------------
+  if constexpr (PERSIST) {
+    int n_items;
+    if constexpr (TABLE) {
+      // Chunk prefix over sequences (block-wide exclusive scan), once.
+      int carry = 0;
+      for (int base = 0; base < p.B; base += kThreads) {
+        const int bb = base + tid;
+        int n = 0, len = 0, ps = 0;
+        if (bb < p.B) {
+          ps = p.indptr[bb];
+          len = paged_len(p.indptr, p.last_len, bb, p.page_size);
+          n = (len + p.chunk - 1) / p.chunk;
+        }
+        int incl = n;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+          const int t = __shfl_up(incl, off, 64);
+          if (lane >= off) incl += t;
+        }
+        if (lane == 63) sm_wtot[wave] = incl;
+        __syncthreads();
+        int before = carry, total = carry;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+          before += (w < wave) ? sm_wtot[w] : 0;
+          total += sm_wtot[w];
+        }
+        if (bb < p.B) {
+          sm_cs[bb] = before + incl - n;
+          sm_len[bb] = len;
+          sm_ps[bb] = ps;
+        }
+        carry = total;
+        __syncthreads();
+      }
+      if (tid == 0) sm_cs[p.B] = carry;
+      __syncthreads();
+      n_items = sm_cs[p.B] * Y;
     } else {
-      p.part_o[(pidx * GT + h) * D + d] = O;
-      if (d == 0) {
-        float* ml = p.part_ml + (pidx * GT + h) * 4;
-        ml[0] = M;
-        ml[1] = L;
-        ml[2] = E;
-        ml[3] = 0.f;
+      n_items = p.B * ((p.S + p.chunk - 1) / p.chunk) * Y;
+    }
+    // Dynamic schedule: workgroup w starts with items w and w + gridDim.x,
+    // then takes tickets 2 * gridDim.x, 2 * gridDim.x + 1, ... from
+    // counters[0], two items ahead so the atomic's latency is hidden (and
+    // the first two items need no atomic at all).  The last workgroup to
+    // exit resets both counters to zero for the next launch.
+    int i = blockIdx.x;
+    int nxt = i + (int)gridDim.x;
+    int pending = 0;
+    if (i < n_items) {  // workgroup-uniform; the grid is sized from an upper bound
+    Item nx;
+    IssueCtx cc, nc;
+    half8_t qn[KS];
+    it = resolve_persistent(i);
+    make_uniform(it);
+    setup(it, cc, qf);
+    nx = resolve_persistent(nxt < n_items ? nxt : i);
+    make_uniform(nx);
+    setup(nx, nc, qn);
+    Buf bufs[2];
+    issue(cc, cc.g_begin + wave, bufs[0]);
+    issue(cc, cc.g_begin + wave + kWaves, bufs[1]);
+    for (;;) {
+      if (tid == 0) pending = 2 * (int)gridDim.x + atomicAdd(&p.counters[0], 1);
+      begin_item();
+      // Groups k of this item; the prefetch two groups ahead crosses into the
+      // next item for the last two (k + 2 >= GPW is a compile-time condition).
+#pragma unroll
+      for (int k = 0; k < GPW; ++k) {
+        consume(bufs[k & 1]);
+        if (k + 2 < GPW) issue(cc, cc.g_begin + wave + kWaves * (k + 2), bufs[k & 1]);
+        else issue(nc, nc.g_begin + wave + kWaves * (k + 2 - GPW), bufs[k & 1]);
+      }
+      if (tid == 0) sm_next = pending;  // published by finish()'s first barrier
+      finish();
+      const int inext = nxt;
+      nxt = sm_next;
+      if (inext >= n_items) break;  // the last prefetch re-read this item (L2 hits)
+      i = inext;
+      it = nx;
+      cc = nc;
+#pragma unroll
+      for (int s = 0; s < KS; ++s) qf[s] = qn[s];
+      nx = resolve_persistent(nxt < n_items ? nxt : i);
+      make_uniform(nx);
+      setup(nx, nc, qn);
+    }
+    }  // i < n_items
+    if (tid == 0) {
+      if (atomicAdd(&p.counters[1], 1) == (int)gridDim.x - 1) {
+        atomicExch(&p.counters[0], 0);
+        atomicExch(&p.counters[1], 0);
       }
     }
+  } else {
+    it = resolve_block();
+    if (it.b < 0) return;  // workgroup-uniform
+    make_uniform(it);
+    IssueCtx cc;
+    setup(it, cc, qf);
+    begin_item();
+    const int g_end = (it.t1 + 15) >> 4;
+    if constexpr (GPW > 0) {
+      Buf bufs[2];
+      const int gw = cc.g_begin + wave;
+      issue(cc, gw, bufs[0]);
+#pragma unroll
+      for (int k = 0; k < GPW; ++k) {
+        if (k + 1 < GPW) issue(cc, gw + kWaves * (k + 1), bufs[(k + 1) & 1]);
+        consume(bufs[k & 1]);
+      }
+    } else {
+      // Dynamic group count (sparse units): ping-pong over two buffers.  The
+      // last prefetch re-reads the current group (an L2 hit) so that every
+      // iteration issues the same loads.
+      int g = cc.g_begin + wave;
+      if (g < g_end) {
+        Buf A, B;
+        issue(cc, g, A);
+        for (;;) {
+          int gn = g + kWaves;
+          issue(cc, gn < g_end ? gn : g, B);
+          consume(A);
+          if (gn >= g_end) break;
+          g = gn;
+          gn = g + kWaves;
+          issue(cc, gn < g_end ? gn : g, A);
+          consume(B);
+          if (gn >= g_end) break;
+          g = gn;
+        }
+      }
+    }
+    finish();
   }
 }
 
@@ -510,7 +754,19 @@ __global__ __launch_bounds__(kThreads) void split_kernel(SplitParams p) {
 // ---------------------------------------------------------------------------
 template <int D, int GT, int MODE>
 __global__ __launch_bounds__(kThreads) void split_combine_kernel(SplitParams p) {
+  // One workgroup merges the partials of one unit (GT heads x D dims).  All
+  // loads of a phase are independent of each other, so the workgroup keeps
+  // many of them in flight instead of walking the chunks one by one.
   constexpr bool SPARSE = (MODE == kModeSparseDense || MODE == kModeSparsePaged);
+  constexpr int NV = GT * D / 4;                          // float4 output vectors
+  constexpr int NG = NV >= kThreads ? 1 : kThreads / NV;  // chunk groups in phase 3
+  constexpr int CAP = 2048 / GT;                          // chunk weights kept in LDS
+  __shared__ float sm_w[CAP * GT];
+  __shared__ float sm_red[kThreads];
+  __shared__ float sm_M[GT], sm_L[GT], sm_E[GT];
+  __shared__ float4_t sm_o[NG > 1 ? kThreads : 1];
+
+  const int tid = threadIdx.x;
   int b, hq0, nh, nch;
   int64_t first, step;
   if constexpr (SPARSE) {
@@ -519,7 +775,6 @@ __global__ __launch_bounds__(kThreads) void split_combine_kernel(SplitParams p) 
     hq0 = u - b * p.Hq;
     nh = 1;
     nch = p.n_split;
-    if (nch == 1) return;
     first = (int64_t)u * p.n_split;
     step = 1;
   } else {
@@ -536,28 +791,138 @@ __global__ __launch_bounds__(kThreads) void split_combine_kernel(SplitParams p) 
     } else {
       chunk_span(p, b, cs, nch);
     }
-    if (nch == 1) return;
     first = (int64_t)cs * gridDim.y + y;
     step = gridDim.y;
   }
-  for (int idx = threadIdx.x; idx < nh * D; idx += kThreads) {
-    const int h = idx / D;
-    const int d = idx - h * D;
+  if (nch == 1) return;  // the split kernel wrote this unit's output directly
+  if (nch == 0) {        // empty unit: no partials exist
+    for (int idx = tid; idx < nh * D; idx += kThreads) {
+      const int h = idx / D;
+      const int64_t row = (int64_t)b * p.Hq + hq0 + h;
+      p.o[row * D + (idx - h * D)] = (half_t)0.f;
+      if (idx - h * D == 0 && p.lse) p.lse[row] = AKT_NEG_INF;
+    }
+    return;
+  }
+  auto ml = [&](int c, int h) -> float4_t {
+    return *reinterpret_cast<const float4_t*>(p.part_ml + ((first + c * step) * GT + h) * 4);
+  };
+
+  // Phase 0: issue the first U chunk rows of partial outputs for this
+  // thread's float4 before anything else, so these loads overlap the
+  // (m, l, e) loads of phases 1-2 (one round trip instead of three).
+  constexpr int U = 8;
+  constexpr int VSTEP = kThreads / NG;  // output vectors per pass
+  constexpr int NPASS = (NV + VSTEP - 1) / VSTEP;
+  const int cg = tid / VSTEP;
+  float4_t ov[NPASS][U];
+#pragma unroll
+  for (int ps = 0; ps < NPASS; ++ps) {
+    const int vec = min(ps * VSTEP + tid % VSTEP, NV - 1);
+    const int h = (vec * 4) / D;
+    const int d0 = vec * 4 - h * D;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int c = max(0, min(cg + u * NG, nch - 1));
+      ov[ps][u] = *reinterpret_cast<const float4_t*>(
+          p.part_o + ((first + c * step) * GT + h) * D + d0);
+    }
+  }
+
+  // Phase 1: per-head max over chunks.  Thread t serves head t % GT.
+  const int h1 = tid % GT;
+  float mloc = AKT_NEG_INF;
+  for (int c = tid / GT; c < nch; c += kThreads / GT) mloc = fmaxf(mloc, ml(c, h1)[0]);
+  sm_red[tid] = mloc;
+  __syncthreads();
+  if (tid < GT) {
     float M = AKT_NEG_INF;
-    for (int c = 0; c < nch; ++c) M = fmaxf(M, p.part_ml[((first + c * step) * GT + h) * 4]);
-    float L = 0.f, E = 0.f, O = 0.f;
-    if (M != AKT_NEG_INF) {
-      for (int c = 0; c < nch; ++c) {
-        const int64_t pi = (first + c * step) * GT + h;
-        const float f = fast_exp2(p.part_ml[pi * 4] - M);
-        L += f * p.part_ml[pi * 4 + 1];
-        E += f * p.part_ml[pi * 4 + 2];
-        O += f * p.part_o[pi * D + d];
+    for (int i = tid; i < kThreads; i += GT) M = fmaxf(M, sm_red[i]);
+    sm_M[tid] = M;
+  }
+  __syncthreads();
+
+  // Phase 2: chunk weights 2^(m_c - M) and the two normalisers.
+  const float M1 = sm_M[h1];
+  float lloc = 0.f, eloc = 0.f;
+  for (int c = tid / GT; c < nch; c += kThreads / GT) {
+    const float4_t v = ml(c, h1);
+    const float w = (M1 == AKT_NEG_INF) ? 0.f : fast_exp2(v[0] - M1);
+    if (c < CAP) sm_w[c * GT + h1] = w;
+    lloc += w * v[1];
+    eloc += w * v[2];
+  }
+  sm_red[tid] = lloc;
+  __syncthreads();
+  if (tid < GT) {
+    float L = 0.f;
+    for (int i = tid; i < kThreads; i += GT) L += sm_red[i];
+    sm_L[tid] = L;
+  }
+  __syncthreads();
+  sm_red[tid] = eloc;
+  __syncthreads();
+  if (tid < GT) {
+    float E = 0.f;
+    for (int i = tid; i < kThreads; i += GT) E += sm_red[i];
+    sm_E[tid] = E;
+  }
+  __syncthreads();
+
+  // Phase 3: weighted sum of the partial outputs (the first U chunk rows are
+  // already in registers), NG chunk groups reduced through LDS.
+  auto weight = [&](int c, int h, float Mh) -> float {
+    if (c < CAP) return sm_w[c * GT + h];
+    return (Mh == AKT_NEG_INF) ? 0.f : fast_exp2(ml(c, h)[0] - Mh);
+  };
+#pragma unroll
+  for (int ps = 0; ps < NPASS; ++ps) {
+    const int vec = ps * VSTEP + tid % VSTEP;
+    const int h = (min(vec, NV - 1) * 4) / D;
+    const int d0 = min(vec, NV - 1) * 4 - h * D;
+    const float Mh = sm_M[h];
+    float4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int c = cg + u * NG;
+      if (c < nch) acc += weight(c, h, Mh) * ov[ps][u];
+    }
+    // Remaining chunks in batches of U independent loads (one round trip each).
+    for (int c0 = cg + U * NG; c0 < nch; c0 += U * NG) {
+      float4_t ob[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int c = min(c0 + u * NG, nch - 1);
+        ob[u] = *reinterpret_cast<const float4_t*>(
+            p.part_o + ((first + c * step) * GT + h) * D + d0);
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int c = c0 + u * NG;
+        if (c < nch) acc += weight(c, h, Mh) * ob[u];
       }
     }
-    const int64_t row = (int64_t)b * p.Hq + hq0 + h;
-    p.o[row * D + d] = (half_t)(L > 0.f ? O / L : 0.f);
-    if (d == 0 && p.lse) p.lse[row] = E > 0.f ? (M + log2f(E)) * kLn2 : AKT_NEG_INF;
+    if constexpr (NG > 1) {
+      sm_o[tid] = acc;
+      __syncthreads();
+      if (cg == 0) {
+        for (int i = 1; i < NG; ++i) acc += sm_o[tid + i * VSTEP];
+      }
+      __syncthreads();
+    }
+    if (cg == 0 && vec < NV && h < nh) {
+      const float L = sm_L[h];
+      const float inv = L > 0.f ? 1.0f / L : 0.f;
+      const int64_t row = (int64_t)b * p.Hq + hq0 + h;
+      half4_t hv;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) hv[r] = (half_t)(acc[r] * inv);
+      *reinterpret_cast<half4_t*>(p.o + row * D + d0) = hv;
+      if (d0 == 0 && p.lse) {
+        const float E = sm_E[h];
+        p.lse[row] = E > 0.f ? (sm_M[h] + log2f(E)) * kLn2 : AKT_NEG_INF;
+      }
+    }
   }
 }
 
@@ -573,14 +938,65 @@ int pick_gt(int G, int D) {
   return gt;
 }
 
+// Workgroups of `kernel` that fit the current device at once (occupancy x CUs),
+// cached per kernel instance and device.
+template <typename Kernel>
+int resident_blocks(Kernel kernel) {
+  static std::atomic<int> cache[kMaxDevices];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 0;
+  int v = cache[dev].load(std::memory_order_relaxed);
+  if (v > 0) return v;
+  int per_cu = 0, cus = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void*)kernel, kThreads, 0) !=
+          hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    return 0;
+  v = (per_cu > 0 ? per_cu : 1) * (cus > 0 ? cus : 1);
+  cache[dev].store(v, std::memory_order_relaxed);
+  return v;
+}
+
+// Launches one split-kernel instance.  Persistent instances get a grid of
+// min(items, resident workgroups); `grid` carries the item upper bound in x.
+template <int D, int GT, int MODE, bool ALIGNED, bool MAGIC, int GPW, bool PERSIST>
+int launch_split(const SplitParams& p, dim3 grid, hipStream_t st) {
+  auto kernel = split_kernel<D, GT, MODE, ALIGNED, MAGIC, GPW, PERSIST>;
+  if (PERSIST) {
+    const int64_t items = (int64_t)grid.x * grid.y;
+    const int cap = resident_blocks(kernel);
+    if (cap <= 0) return set_error(AKT_ERR_HIP, "occupancy query failed");
+    grid = dim3((unsigned)(items < cap ? items : cap), 1);
+  }
+  KernelTimer timer(st);
+  hipLaunchKernelGGL(kernel, grid, dim3(kThreads), 0, st, p);
+  timer.stop();
+  return check_launch("split_kernel");
+}
+
 template <int D, int GT, int MODE, bool ALIGNED, bool MAGIC>
 int launch_t(const SplitParams& p, dim3 grid, dim3 cgrid, hipStream_t st) {
+  constexpr bool SPARSE = (MODE == kModeSparseDense || MODE == kModeSparsePaged);
   int rc = AKT_OK;
   if (grid.x > 0 && grid.y > 0) {
-    KernelTimer timer(st);
-    hipLaunchKernelGGL((split_kernel<D, GT, MODE, ALIGNED, MAGIC>), grid, dim3(kThreads), 0, st, p);
-    timer.stop();
-    rc = check_launch("split_kernel");
+    if constexpr (SPARSE) {
+      rc = launch_split<D, GT, MODE, ALIGNED, MAGIC, 0, false>(p, grid, st);
+    } else if constexpr (MODE == kModePaged && !ALIGNED) {
+      // Pages that do not hold whole 16-token groups: 256-token chunks only.
+      if (p.B <= kMaxTableB) rc = launch_split<D, GT, MODE, false, MAGIC, 4, true>(p, grid, st);
+      else rc = launch_split<D, GT, MODE, false, MAGIC, 4, false>(p, grid, st);
+    } else {
+      // A chunk of `chunk` tokens is chunk / 64 16-token groups per wave.
+      bool persist = true;
+      if constexpr (MODE == kModePaged) persist = p.B <= kMaxTableB;
+      if constexpr (MODE == kModePaged) {
+        if (!persist) rc = launch_split<D, GT, MODE, ALIGNED, MAGIC, 4, false>(p, grid, st);
+      }
+      if (!persist) {
+      } else if (p.chunk == 128) rc = launch_split<D, GT, MODE, ALIGNED, MAGIC, 2, true>(p, grid, st);
+      else if (p.chunk == 256) rc = launch_split<D, GT, MODE, ALIGNED, MAGIC, 4, true>(p, grid, st);
+      else rc = launch_split<D, GT, MODE, ALIGNED, MAGIC, 8, true>(p, grid, st);
+    }
     if (rc) return rc;
   }
   if (cgrid.x > 0 && cgrid.y > 0) {
@@ -618,11 +1034,23 @@ int launch_d(int D, int gt, const SplitParams& p, dim3 grid, dim3 cgrid, hipStre
   return set_error(AKT_ERR_UNSUPPORTED, "head_dim %d not supported (64, 128, 256)", D);
 }
 
-// Automatic chunk length for dense / paged caches: aim for ~4096 workgroups.
+// Automatic chunk length for dense / paged caches: the smallest supported
+// length (128, 256, 512) that keeps the item count near 4096.
 int64_t auto_chunk(int64_t total_tokens, int64_t units) {
-  int64_t c = ceil_div(total_tokens * units, 4096);
-  c = round_up(c < 64 ? 64 : c, 64);
-  return c > 4096 ? 4096 : c;
+  const int64_t want = ceil_div(total_tokens * units, 4096);
+  int64_t c = 128;
+  while (c < want && c < kMaxChunk) c <<= 1;
+  return c;
+}
+
+bool chunk_ok(int64_t c) { return c == 0 || c == 128 || c == 256 || c == 512; }
+
+// Chunk length of a paged launch: pages that do not hold whole 16-token
+// groups and batches past the LDS chunk table use 256-token chunks.
+int64_t paged_chunk(int64_t chunk_tokens, int64_t total_pages, int64_t page_size, int64_t Y,
+                    int64_t batch) {
+  if (page_size % 16 != 0 || batch > kMaxTableB) return 256;
+  return chunk_tokens > 0 ? chunk_tokens : auto_chunk(total_pages * page_size, Y);
 }
 
 int64_t auto_splits(int64_t rows, int64_t l_max) {
@@ -663,7 +1091,7 @@ extern "C" size_t akt_decode_workspace_size(int64_t batch, int64_t num_q_heads,
   const int64_t units = batch * num_kv_heads * n_hg;
   const int64_t chunk = chunk_tokens > 0 ? chunk_tokens : auto_chunk(seq_len * batch, num_kv_heads * n_hg);
   const int64_t nch = ceil_div(seq_len, chunk);
-  return nch > 1 ? split_ws_bytes(units * nch, gt, head_dim) : 0;
+  return kCounterBytes + (nch > 1 ? split_ws_bytes(units * nch, gt, head_dim) : 0);
 }
 
 extern "C" int akt_decode_fwd(const void* q, const void* k, const void* v, void* o, float* lse,
@@ -680,7 +1108,7 @@ extern "C" int akt_decode_fwd(const void* q, const void* k, const void* v, void*
   AKT_CHECK(rows_aligned16(q, q_stride, 3) && rows_aligned16(k, k_stride, 3) &&
                 rows_aligned16(v, v_stride, 3) && aligned16(o),
             "tensors must have 16-byte aligned rows");
-  AKT_CHECK(chunk_tokens >= 0 && chunk_tokens % 64 == 0, "chunk_tokens must be a multiple of 64");
+  AKT_CHECK(chunk_ok(chunk_tokens), "chunk_tokens must be 0 (automatic), 128, 256 or 512");
   if (batch == 0) return AKT_OK;
   const int D = (int)head_dim;
   const int G = (int)(num_q_heads / num_kv_heads);
@@ -690,8 +1118,8 @@ extern "C" int akt_decode_fwd(const void* q, const void* k, const void* v, void*
                                          : auto_chunk(seq_len * batch, num_kv_heads * n_hg);
   const int64_t nch = ceil_div(seq_len, chunk);
   const int64_t Y = num_kv_heads * n_hg;
-  const size_t need = nch > 1 ? split_ws_bytes(batch * Y * nch, gt, D) : 0;
-  if (need && (!workspace || workspace_bytes < need))
+  const size_t need = kCounterBytes + (nch > 1 ? split_ws_bytes(batch * Y * nch, gt, D) : 0);
+  if (!workspace || workspace_bytes < need)
     return set_error(AKT_ERR_WORKSPACE, "workspace of %zu bytes required", need);
 
   SplitParams p = {};
@@ -700,8 +1128,9 @@ extern "C" int akt_decode_fwd(const void* q, const void* k, const void* v, void*
   p.vbase = (const half_t*)v;
   p.o = (half_t*)o;
   p.lse = lse;
-  p.part_o = (float*)workspace;
-  p.part_ml = p.part_o + (need ? (size_t)batch * Y * nch * gt * D : 0);
+  p.counters = (int*)workspace;
+  p.part_o = (float*)((char*)workspace + kCounterBytes);
+  p.part_ml = p.part_o + (nch > 1 ? (size_t)batch * Y * nch * gt * D : 0);
   p.q_sb = q_stride[0];
   p.q_sh = q_stride[1];
   p.k_sa = k_stride[2]; p.k_sb = 0; p.k_batch = k_stride[0]; p.k_head = k_stride[1];
@@ -733,8 +1162,9 @@ extern "C" size_t akt_decode_paged_workspace_size(int64_t batch, int64_t num_q_h
   const int G = (int)(num_q_heads / num_kv_heads);
   const int gt = pick_gt(G, (int)head_dim);
   const int64_t Y = num_kv_heads * ceil_div(G, gt);
-  const int64_t chunk = chunk_tokens > 0 ? chunk_tokens : auto_chunk(total_pages * page_size, Y);
-  return split_ws_bytes(paged_grid_x(total_pages, page_size, chunk, batch) * Y, gt, head_dim);
+  const int64_t chunk = paged_chunk(chunk_tokens, total_pages, page_size, Y, batch);
+  return kCounterBytes +
+         split_ws_bytes(paged_grid_x(total_pages, page_size, chunk, batch) * Y, gt, head_dim);
 }
 
 extern "C" int akt_decode_paged_fwd(const void* q, const void* kv_cache,
@@ -755,16 +1185,16 @@ extern "C" int akt_decode_paged_fwd(const void* q, const void* kv_cache,
   AKT_CHECK(q_stride[3] == 1 && kv_stride[4] == 1, "head_dim stride must be 1");
   AKT_CHECK(rows_aligned16(q, q_stride, 3) && rows_aligned16(kv_cache, kv_stride, 4) && aligned16(o),
             "tensors must have 16-byte aligned rows");
-  AKT_CHECK(chunk_tokens >= 0 && chunk_tokens % 64 == 0, "chunk_tokens must be a multiple of 64");
+  AKT_CHECK(chunk_ok(chunk_tokens), "chunk_tokens must be 0 (automatic), 128, 256 or 512");
   if (batch == 0) return AKT_OK;
   const int D = (int)head_dim;
   const int G = (int)(num_q_heads / num_kv_heads);
   const int gt = pick_gt(G, D);
   const int n_hg = (int)ceil_div(G, gt);
   const int64_t Y = num_kv_heads * n_hg;
-  const int64_t chunk = chunk_tokens > 0 ? chunk_tokens : auto_chunk(total_pages * page_size, Y);
+  const int64_t chunk = paged_chunk(chunk_tokens, total_pages, page_size, Y, batch);
   const int64_t gx = paged_grid_x(total_pages, page_size, chunk, batch);
-  const size_t need = split_ws_bytes(gx * Y, gt, D);
+  const size_t need = kCounterBytes + split_ws_bytes(gx * Y, gt, D);
   if (!workspace || workspace_bytes < need)
     return set_error(AKT_ERR_WORKSPACE, "workspace of %zu bytes required", need);
 
@@ -777,7 +1207,8 @@ extern "C" int akt_decode_paged_fwd(const void* q, const void* kv_cache,
   p.last_len = kv_last_page_len;
   p.o = (half_t*)o;
   p.lse = lse;
-  p.part_o = (float*)workspace;
+  p.counters = (int*)workspace;
+  p.part_o = (float*)((char*)workspace + kCounterBytes);
   p.part_ml = p.part_o + (size_t)gx * Y * gt * D;
   p.q_sb = q_stride[0];
   p.q_sh = q_stride[1];
@@ -803,7 +1234,7 @@ extern "C" size_t akt_sparse_decode_workspace_size(int64_t batch, int64_t num_q_
   if (batch <= 0 || num_q_heads <= 0 || !head_dim_ok(head_dim)) return 0;
   const int64_t rows = batch * num_q_heads;
   const int64_t ns = num_splits > 0 ? num_splits : auto_splits(rows, l_max);
-  return ns > 1 ? split_ws_bytes(rows * ns, 1, head_dim) : 0;
+  return kCounterBytes + (ns > 1 ? split_ws_bytes(rows * ns, 1, head_dim) : 0);
 }
 
 namespace {
@@ -822,16 +1253,17 @@ int sparse_common(SplitParams& p, const void* q, const int32_t* sparse_ind,
   AKT_CHECK(num_splits >= 0, "num_splits must be >= 0");
   const int64_t rows = batch * num_q_heads;
   const int64_t ns = num_splits > 0 ? num_splits : auto_splits(rows, l_max);
-  const size_t need = ns > 1 ? split_ws_bytes(rows * ns, 1, head_dim) : 0;
-  if (need && (!workspace || workspace_bytes < need))
+  const size_t need = kCounterBytes + (ns > 1 ? split_ws_bytes(rows * ns, 1, head_dim) : 0);
+  if (!workspace || workspace_bytes < need)
     return set_error(AKT_ERR_WORKSPACE, "workspace of %zu bytes required", need);
   p.q = (const half_t*)q;
   p.sparse_ind = sparse_ind;
   p.sparse_nnz = sparse_nnz;
   p.o = (half_t*)o;
   p.lse = lse;
-  p.part_o = (float*)workspace;
-  p.part_ml = p.part_o + (need ? (size_t)rows * ns * head_dim : 0);
+  p.counters = (int*)workspace;
+  p.part_o = (float*)((char*)workspace + kCounterBytes);
+  p.part_ml = p.part_o + (ns > 1 ? (size_t)rows * ns * head_dim : 0);
   p.q_sb = q_stride[0];
   p.q_sh = q_stride[1];
   p.ind_sb = ind_stride[0];

@@ -1,33 +1,37 @@
 // Causal / non-causal GQA flash-attention prefill for gfx950.
 //
 // Replaces the reference's Triton prefill kernels
-//   prefill_flash_attention.py:18-335           (dense)
+//   prefill_flash_attention.py:18-335                   (dense)
 //   prefill_flash_attention_var_len_padding.py:109-341  (right-padded var-len)
-// with an MFMA kernel designed around CDNA4's v_mfma_f32_32x32x16_f16.
+// with an MFMA kernel designed around CDNA4's v_mfma_f32_32x32x16_f16 and its
+// transposing LDS read (ds_read_b64_tr_b16).
 //
-// Tiling.  A 256-thread workgroup owns 128 query rows of one (batch, q head);
-// wave w owns rows 32w..32w+31.  Keys stream through LDS in 64-key tiles:
-//   sK  : K tile, row-major [key][dim] (row padded by 16 bytes)
-//   sVt : V tile transposed [dim][key] (row padded by 16 bytes) with the key
-//         order permuted so that each MFMA operand read is one 16-byte access.
-// Both products are computed transposed so that each lane owns one query row:
-//   S^T = K . Q^T    (A = K from LDS, B = Q^T held in registers)
-//   O^T = V^T . P^T  (A = V^T from LDS, B = P^T straight from the S^T registers)
-// With the 32x32 result layout, lane l holds query row l & 31 and 16 key (or
-// dim) slots; the two 32-lane halves hold complementary slots, so the row max
-// and row sum need one exchange between lane l and l ^ 32.
+// Work decomposition.  A 256-thread workgroup serves one (batch, kv head) and
+// four "slots"; slot f = (query head f % G, 64-row block f / G) of that kv
+// head's G query heads.  With G a multiple of 4 the four waves are four query
+// heads at the same rows: they share every staged K/V tile and have identical
+// causal extents.  Each wave owns 64 query rows as two 32-row MFMA blocks that
+// share every K and V fragment read from LDS.
 //
-// Softmax.  Scores are scaled by softmax_scale * log2(e) and exponentiated
-// with v_exp_f32.  The running max is only raised when a tile's max exceeds it
-// by more than kRescaleSlack (in log2 units); otherwise the stale max is kept,
-// which bounds P by 2^kRescaleSlack and skips the O rescale.  P is rounded to
-// fp16 for the P.V product (as the reference does at prefill_flash_attention.py:94)
+// Per 64-key tile, staged row-major in LDS (sK, sV, rows padded by 16 bytes):
+//   S^T = K . Q^T    A = K rows from LDS (16-byte reads), B = Q^T in registers
+//   O^T = V^T . P^T  A = V^T via ds_read_b64_tr_b16 from the row-major V tile,
+//                    B = P^T taken straight from the S^T registers
+// Computing both products transposed makes each lane own one query row (lane &
+// 31) of each 32-row block; the two 32-lane halves hold complementary key (or
+// dim) slots, so row max / sum need one exchange between lane l and l ^ 32.
+//
+// Softmax.  Scores are scaled by softmax_scale * log2(e) and exponentiated with
+// v_exp_f32, 32 keys at a time.  The running max is only raised when a tile's
+// max exceeds it by more than kRescaleSlack (log2 units); otherwise the stale
+// max is kept, which bounds P by 2^kRescaleSlack and skips the O rescale.  P is
+// rounded to fp16 for P.V (as the reference does at prefill_flash_attention.py:94)
 // and the normaliser sums the same rounded values.
 //
-// Masking uses a select (score = -inf), not an additive -1e6 as in the
-// reference (prefill_flash_attention.py:76), so non-finite padding never leaks.
-// In var-len causal mode the K/V rows at or beyond a sequence's length are
-// staged as zeros, so padding cannot reach valid rows through P.V either.
+// Masking uses a select (score = -inf), not the reference's additive -1e6
+// (prefill_flash_attention.py:76), so non-finite padding never leaks.  In
+// var-len causal mode the K/V rows at or beyond a sequence's length are staged
+// as zeros, so padding cannot reach valid rows through P.V either.
 #include <math.h>
 
 #include "akt_common.hpp"
@@ -38,8 +42,9 @@ namespace akt {
 namespace {
 
 constexpr int kPThreads = 256;
-constexpr int kBM = 128;  // query rows per workgroup
-constexpr int kBN = 64;   // keys per tile
+constexpr int kSlots = 4;   // waves per workgroup
+constexpr int kRows = 64;   // query rows per slot (two 32-row MFMA blocks)
+constexpr int kBN = 64;     // keys per staged tile
 constexpr float kRescaleSlack = 8.0f;
 #define AKT_P_NEG_INF (-__builtin_inff())
 
@@ -55,69 +60,68 @@ struct PrefillParams {
   int64_t o_sb, o_sh, o_ss;
   int B, Hq, Hkv, G, S;
   int varlen_bits;
-  int n_qblk;    // query blocks per head
-  int xcd_map;   // 1: group kv heads per XCD (requires (B*Hkv) % 8 == 0)
+  int n_rb;      // 64-row blocks per sequence
+  int n_sg;      // slot groups (workgroups) per (batch, kv head)
+  int xcd_map;   // 1: keep a kv head's workgroups on one XCD (needs (B*Hkv) % 8 == 0)
   float qk_scale;  // softmax_scale * log2(e)
 };
 
-// Key position inside a 64-key sVt row: swaps bits 2 and 3 of the key index so
-// that the 8 keys one lane feeds to a 32x32x16 MFMA are contiguous.
-__device__ __forceinline__ int vt_pos(int key) {
-  return (key & ~15) | ((key & 4) << 1) | ((key & 8) >> 1) | (key & 3);
+typedef short short4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) short4_t lds_short4;
+
+// ds_read_b64_tr_b16: within each 16-lane group, output lane i, element j is
+// component (i % 4) of the 8-byte chunk addressed by source lane 4j + i / 4.
+// If source lane s addresses row k0 + s / 4, columns c0 + 4 (s % 4) .. +3 of a
+// row-major fp16 matrix, output lane i receives rows k0..k0+3 of column c0 + i.
+__device__ __forceinline__ uint2 ds_read_tr16(const half_t* lds_ptr) {
+  const short4_t r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4*)(lds_ptr));
+  return __builtin_bit_cast(uint2, r);
 }
 
-// Workgroup -> (batch, q head, query block).  Causal work is issued heaviest
-// block first; with xcd_map the workgroups of one kv head land on one XCD
-// (workgroup i is dispatched to XCD i % 8) so its L2 serves the G query heads.
-__device__ __forceinline__ void map_block(const PrefillParams& p, bool causal, int& b, int& h,
-                                          int& qb) {
+// Workgroup -> (batch, kv head, slot group).  Causal work is issued heaviest
+// slot group first; with xcd_map the workgroups of one kv head land on one
+// XCD (workgroup i is dispatched to XCD i % 8) so its L2 serves them all.
+__device__ __forceinline__ void map_block(const PrefillParams& p, bool causal, int& b, int& kvh,
+                                          int& sg) {
   const int pid = blockIdx.x;
-  const int nheads = p.B * p.Hq;
-  int rank, head;
+  const int ngroups = p.B * p.Hkv;
+  int rank, kg;
   if (p.xcd_map) {
     const int xcd = pid & 7;
     const int j = pid >> 3;
-    const int nk = (p.B * p.Hkv) >> 3;  // kv groups per XCD
-    const int per_rank = nk * p.G;
-    rank = j / per_rank;
-    const int rem = j - rank * per_rank;
-    const int kl = rem / p.G;
-    const int g = rem - kl * p.G;
-    const int kg = kl * 8 + xcd;  // global kv group = b * Hkv + kvh
-    head = kg * p.G + g;          // = b * Hq + kvh * G + g
+    const int nk = ngroups >> 3;  // kv groups per XCD
+    rank = j / nk;
+    kg = (j - rank * nk) * 8 + xcd;
   } else {
-    rank = pid / nheads;
-    head = pid - rank * nheads;
+    rank = pid / ngroups;
+    kg = pid - rank * ngroups;
   }
-  b = head / p.Hq;
-  h = head - b * p.Hq;
-  qb = causal ? (p.n_qblk - 1 - rank) : rank;
+  b = kg / p.Hkv;
+  kvh = kg - b * p.Hkv;
+  sg = causal ? (p.n_sg - 1 - rank) : rank;
 }
 
 template <int D, bool CAUSAL, bool VARLEN>
-__global__ __launch_bounds__(kPThreads) void prefill_kernel(PrefillParams p) {
+__global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(D == 64 ? 2 : 1, 2))) void prefill_kernel(PrefillParams p) {
   constexpr int KS = D / 16;       // MFMA k-steps over the head dim
   constexpr int HALF = D / 2;      // head dims per lane half in S^T operands
-  constexpr int KROW = D + 8;      // sK row pitch (halfs)
-  constexpr int VROW = kBN + 8;    // sVt row pitch (halfs)
+  constexpr int ROW = D + 8;       // sK / sV row pitch (halfs)
   constexpr int NT = D / 32;       // 32-dim output tiles
-  constexpr int K_CHUNKS = kBN * D / 8;         // 16-byte chunks per K tile
-  constexpr int V_PAIRS = (kBN / 2) * (D / 8);  // (key pair, 8 dims) chunks per V tile
-  constexpr int K_PER_T = K_CHUNKS / kPThreads;
-  constexpr int V_PER_T = V_PAIRS / kPThreads;
-  static_assert(K_CHUNKS % kPThreads == 0 && V_PAIRS % kPThreads == 0, "tile split");
+  constexpr int CHUNKS = kBN * D / 8;  // 16-byte chunks per K (or V) tile
+  constexpr int PER_T = CHUNKS / kPThreads;
+  static_assert(CHUNKS % kPThreads == 0, "tile split");
 
-  __shared__ __attribute__((aligned(16))) half_t sK[kBN * KROW];
-  __shared__ __attribute__((aligned(16))) half_t sVt[D * VROW];
+  __shared__ __attribute__((aligned(16))) half_t sK[kBN * ROW];
+  __shared__ __attribute__((aligned(16))) half_t sV[kBN * ROW];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = uniform(tid >> 6);
   const int l32 = lane & 31;
   const int g = lane >> 5;
 
-  int b, h, qb;
-  map_block(p, CAUSAL, b, h, qb);
+  int b, kvh, sg;
+  map_block(p, CAUSAL, b, kvh, sg);
   const int S = p.S;
   int len = S;
   if constexpr (VARLEN) {
@@ -128,93 +132,91 @@ __global__ __launch_bounds__(kPThreads) void prefill_kernel(PrefillParams p) {
   // Rows are computed in 64-row blocks up to ceil(len / 64) * 64, as the
   // reference does (prefill_flash_attention_var_len_padding.py:185-187).
   const int row_lim = VARLEN ? min(S, ((len + 63) / 64) * 64) : S;
-  const int q0 = qb * kBM;
-  if (q0 >= row_lim) return;
-  const int kvh = h / p.G;
 
+  // This wave's slot and the workgroup's key range.
+  const int slot = sg * kSlots + wave;
+  const int hl = slot % p.G;
+  const int r0 = (slot / p.G) * kRows;
+  const bool active = slot < p.G * p.n_rb && r0 < row_lim;
+  int kv_end = S;
+  if constexpr (CAUSAL) {
+    int last_r0 = 0;
+    for (int w = 0; w < kSlots; ++w) {
+      const int f = sg * kSlots + w;
+      if (f < p.G * p.n_rb) last_r0 = max(last_r0, (f / p.G) * kRows);
+    }
+    kv_end = min(row_lim, last_r0 + kRows);
+  }
+  const int key_lim = (VARLEN && CAUSAL) ? len : S;  // keys at or past this are staged as zeros
+  const int n_tiles = (kv_end + kBN - 1) / kBN;
+  const int wave_kv_end = CAUSAL ? min(kv_end, r0 + kRows) : kv_end;
+  if (n_tiles == 0) return;
+
+  const int h = kvh * p.G + hl;
   const half_t* __restrict__ Qh = p.q + (int64_t)b * p.q_sb + (int64_t)h * p.q_sh;
   const half_t* __restrict__ Kh = p.k + (int64_t)b * p.k_sb + (int64_t)kvh * p.k_sh;
   const half_t* __restrict__ Vh = p.v + (int64_t)b * p.v_sb + (int64_t)kvh * p.v_sh;
   half_t* __restrict__ Oh = p.o + (int64_t)b * p.o_sb + (int64_t)h * p.o_sh;
 
-  const int qw0 = q0 + 32 * wave;
-  const int row = qw0 + l32;
-  const bool wave_rows = qw0 < row_lim;
-
-  // Q^T fragment: lane -> row, dims g*HALF + 8s + e.
-  half8_t qf[KS];
+  // Q^T fragments of the two 32-row blocks: lane -> row, dims g*HALF + 8s + e.
+  half8_t qf[2][KS];
 #pragma unroll
-  for (int s = 0; s < KS; ++s) {
-    uint4_t v = {0, 0, 0, 0};
-    if (row < S) v = ld16(Qh + (int64_t)row * p.q_ss + g * HALF + 8 * s);
-    qf[s] = as_half8(v);
+  for (int rb = 0; rb < 2; ++rb) {
+    const int row = r0 + 32 * rb + l32;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      uint4_t v = {0, 0, 0, 0};
+      if (active && row < S) v = ld16(Qh + (int64_t)row * p.q_ss + g * HALF + 8 * s);
+      qf[rb][s] = as_half8(v);
+    }
   }
 
-  // Keys this workgroup needs, and keys that must be staged as zeros.
-  int kv_end = S;
-  if constexpr (CAUSAL) kv_end = min(row_lim, q0 + kBM);
-  const int key_lim = (VARLEN && CAUSAL) ? len : S;
-  const int n_tiles = (kv_end + kBN - 1) / kBN;
-  const int wave_kv_end = CAUSAL ? min(kv_end, qw0 + 32) : kv_end;
-
-  float16_t oacc[NT];
+  float16_t oacc[2][NT];
 #pragma unroll
-  for (int n = 0; n < NT; ++n)
+  for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) oacc[n][r] = 0.f;
-  float m_run = AKT_P_NEG_INF;
-  float l_part = 0.f;
+    for (int n = 0; n < NT; ++n)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) oacc[rb][n][r] = 0.f;
+  float m_run[2] = {AKT_P_NEG_INF, AKT_P_NEG_INF};
+  float l_part[2] = {0.f, 0.f};
   const float c = p.qk_scale;
   const uint32_t kOnes = 0x3c003c00u;
 
-  // Staging registers for the next tile.
-  uint4_t kst[K_PER_T];
-  uint4_t vst[V_PER_T][2];
+  // Staging registers for the next tile (row-major 16-byte chunks).
+  uint4_t kst[PER_T], vst[PER_T];
   auto load_tile = [&](int j) {
     const int kbase = j * kBN;
 #pragma unroll
-    for (int i = 0; i < K_PER_T; ++i) {
+    for (int i = 0; i < PER_T; ++i) {
       const int cidx = tid + i * kPThreads;
       const int key = cidx / (D / 8);
       const int dc = cidx - key * (D / 8);
       const int kg = kbase + key;
-      kst[i] = (kg < key_lim) ? ld16(Kh + (int64_t)kg * p.k_ss + 8 * dc) : uint4_t{0, 0, 0, 0};
-    }
-#pragma unroll
-    for (int i = 0; i < V_PER_T; ++i) {
-      const int cidx = tid + i * kPThreads;
-      const int kp = cidx / (D / 8);
-      const int dc = cidx - kp * (D / 8);
-      const int kg = kbase + 2 * kp;
-      vst[i][0] = (kg < key_lim) ? ld16(Vh + (int64_t)kg * p.v_ss + 8 * dc) : uint4_t{0, 0, 0, 0};
-      vst[i][1] =
-          (kg + 1 < key_lim) ? ld16(Vh + (int64_t)(kg + 1) * p.v_ss + 8 * dc) : uint4_t{0, 0, 0, 0};
+      const bool ok = kg < key_lim;
+      kst[i] = ok ? ld16(Kh + (int64_t)kg * p.k_ss + 8 * dc) : uint4_t{0, 0, 0, 0};
+      vst[i] = ok ? ld16(Vh + (int64_t)kg * p.v_ss + 8 * dc) : uint4_t{0, 0, 0, 0};
     }
   };
   auto store_tile = [&]() {
 #pragma unroll
-    for (int i = 0; i < K_PER_T; ++i) {
+    for (int i = 0; i < PER_T; ++i) {
       const int cidx = tid + i * kPThreads;
       const int key = cidx / (D / 8);
       const int dc = cidx - key * (D / 8);
-      *reinterpret_cast<uint4_t*>(&sK[key * KROW + 8 * dc]) = kst[i];
-    }
-#pragma unroll
-    for (int i = 0; i < V_PER_T; ++i) {
-      const int cidx = tid + i * kPThreads;
-      const int kp = cidx / (D / 8);
-      const int dc = cidx - kp * (D / 8);
-      const int pos = vt_pos(2 * kp);
-#pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        const uint32_t a = vst[i][0][w], bb = vst[i][1][w];
-        *reinterpret_cast<uint32_t*>(&sVt[(8 * dc + 2 * w) * VROW + pos]) = pair_lo(a, bb);
-        *reinterpret_cast<uint32_t*>(&sVt[(8 * dc + 2 * w + 1) * VROW + pos]) = pair_hi(a, bb);
-      }
+      *reinterpret_cast<uint4_t*>(&sK[key * ROW + 8 * dc]) = kst[i];
+      *reinterpret_cast<uint4_t*>(&sV[key * ROW + 8 * dc]) = vst[i];
     }
   };
 
-  if (n_tiles > 0) load_tile(0);
+  // V^T fragment addresses: lane l's 16-lane group reads dims d0 + (0..15)
+  // for keys k0..k0+3; source lane s = l % 16 addresses key k0 + s / 4,
+  // dims d0 + 4 (s % 4).
+  const int s16 = lane & 15;
+  const int vt_dim = 16 * ((lane >> 4) & 1) + 4 * (s16 & 3);
+  const int vt_key = s16 >> 2;
+
+  load_tile(0);
   for (int j = 0; j < n_tiles; ++j) {
     __syncthreads();
     store_tile();
@@ -222,93 +224,110 @@ __global__ __launch_bounds__(kPThreads) void prefill_kernel(PrefillParams p) {
     if (j + 1 < n_tiles) load_tile(j + 1);
 
     const int kt0 = j * kBN;
-    if (!wave_rows || kt0 >= wave_kv_end) continue;  // wave-uniform
+    if (!active || kt0 >= wave_kv_end) continue;  // wave-uniform
 
-    // ---- S^T = K . Q^T for the two 32-key halves of the tile ------------
-    float16_t sacc[2];
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
+    for (int hf = 0; hf < 2; ++hf) {
+      const int kh0 = kt0 + 32 * hf;
+      if (kh0 >= wave_kv_end) break;  // wave-uniform: the rest of the tile is masked
+
+      // ---- S^T = K . Q^T for 32 keys x (2 x 32 rows) ------------------------
+      float16_t sacc[2];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) sacc[t][r] = 0.f;
-      const half_t* kr = &sK[(32 * t + l32) * KROW + g * HALF];
+      for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) sacc[rb][r] = 0.f;
+      const half_t* kr = &sK[(32 * hf + l32) * ROW + g * HALF];
 #pragma unroll
       for (int s = 0; s < KS; ++s) {
         const half8_t a = as_half8(*reinterpret_cast<const uint4_t*>(kr + 8 * s));
-        sacc[t] = mfma32x32x16(a, qf[s], sacc[t]);
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb) sacc[rb] = mfma32x32x16(a, qf[rb][s], sacc[rb]);
       }
-    }
 
-    // ---- mask -----------------------------------------------------------
-    const bool need_mask = (CAUSAL && kt0 + kBN - 1 > qw0) || (kt0 + kBN > S);
-    if (need_mask) {
+      // ---- mask ---------------------------------------------------------------
+      const bool need_mask = (CAUSAL && kh0 + 31 > r0) || (kh0 + 32 > S);
+      if (need_mask) {
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
+        for (int rb = 0; rb < 2; ++rb) {
+          const int row = r0 + 32 * rb + l32;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int key = kt0 + 32 * t + 8 * (r >> 2) + 4 * g + (r & 3);
-          const bool ok = (key < S) && (!CAUSAL || key <= row);
-          if (!ok) sacc[t][r] = AKT_P_NEG_INF;
+          for (int r = 0; r < 16; ++r) {
+            const int key = kh0 + 8 * (r >> 2) + 4 * g + (r & 3);
+            const bool ok = (key < S) && (!CAUSAL || key <= row);
+            if (!ok) sacc[rb][r] = AKT_P_NEG_INF;
+          }
         }
-    }
-
-    // ---- online softmax (row = l32) -------------------------------------
-    float mx = sacc[0][0];
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[t][r]);
-    mx = fmaxf(mx, shfl_xor_f(mx, 32)) * c;
-    if (__any(mx > m_run + kRescaleSlack)) {
-      const float m_new = fmaxf(m_run, mx);
-      const float alpha = (m_new > m_run) ? fast_exp2(m_run - m_new) : 1.0f;
-      l_part *= alpha;
-#pragma unroll
-      for (int n = 0; n < NT; ++n)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) oacc[n][r] *= alpha;
-      m_run = m_new;
-    }
-    const float m_use = (m_run == AKT_P_NEG_INF) ? 0.f : m_run;
-    uint32_t pk[2][8];
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int r = 0; r < 16; r += 2) {
-        const float p0 = fast_exp2(__builtin_fmaf(sacc[t][r], c, -m_use));
-        const float p1 = fast_exp2(__builtin_fmaf(sacc[t][r + 1], c, -m_use));
-        pk[t][r >> 1] = pack_half2(p0, p1);
-        l_part = dot2(pk[t][r >> 1], kOnes, l_part);
       }
 
-    // ---- O^T += V^T . P^T -------------------------------------------------
+      // ---- online softmax per 32-row block (row = l32) -------------------------
+      uint32_t pk[2][8];
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+      for (int rb = 0; rb < 2; ++rb) {
+        float mx = sacc[rb][0];
+#pragma unroll
+        for (int r = 1; r < 16; ++r) mx = fmaxf(mx, sacc[rb][r]);
+        mx = fmaxf(mx, shfl_xor_f(mx, 32)) * c;
+        if (__any(mx > m_run[rb] + kRescaleSlack)) {
+          const float m_new = fmaxf(m_run[rb], mx);
+          const float alpha = (m_new > m_run[rb]) ? fast_exp2(m_run[rb] - m_new) : 1.0f;
+          l_part[rb] *= alpha;
+#pragma unroll
+          for (int n = 0; n < NT; ++n)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) oacc[rb][n][r] *= alpha;
+          m_run[rb] = m_new;
+        }
+        const float m_use = (m_run[rb] == AKT_P_NEG_INF) ? 0.f : m_run[rb];
+#pragma unroll
+        for (int r = 0; r < 16; r += 2) {
+          const float p0 = fast_exp2(__builtin_fmaf(sacc[rb][r], c, -m_use));
+          const float p1 = fast_exp2(__builtin_fmaf(sacc[rb][r + 1], c, -m_use));
+          pk[rb][r >> 1] = pack_half2(p0, p1);
+          l_part[rb] = dot2(pk[rb][r >> 1], kOnes, l_part[rb]);
+        }
+      }
+
+      // ---- O^T += V^T . P^T over the 32 keys (two 16-key k-steps) -------------
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
-        const half8_t bop =
-            as_half8(uint4_t{pk[t][4 * u], pk[t][4 * u + 1], pk[t][4 * u + 2], pk[t][4 * u + 3]});
+        half8_t bop[2];
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb)
+          bop[rb] = as_half8(uint4_t{pk[rb][4 * u], pk[rb][4 * u + 1], pk[rb][4 * u + 2],
+                                     pk[rb][4 * u + 3]});
+        const int k0 = 32 * hf + 16 * u + 4 * g + vt_key;
 #pragma unroll
         for (int n = 0; n < NT; ++n) {
-          const half8_t a = as_half8(*reinterpret_cast<const uint4_t*>(
-              &sVt[(32 * n + l32) * VROW + 32 * t + 16 * u + 8 * g]));
-          oacc[n] = mfma32x32x16(a, bop, oacc[n]);
+          const half_t* vp = &sV[k0 * ROW + 32 * n + vt_dim];
+          const uint2 lo = ds_read_tr16(vp);
+          const uint2 hi = ds_read_tr16(vp + 8 * ROW);
+          const half8_t a = as_half8(uint4_t{lo.x, lo.y, hi.x, hi.y});
+#pragma unroll
+          for (int rb = 0; rb < 2; ++rb) oacc[rb][n] = mfma32x32x16(a, bop[rb], oacc[rb][n]);
         }
       }
+    }
   }
 
-  if (!wave_rows || row >= row_lim) return;
-  const float l_row = l_part + shfl_xor_f(l_part, 32);
-  const float inv = l_row > 0.f ? 1.0f / l_row : 0.f;
-  half_t* orow = Oh + (int64_t)row * p.o_ss;
+  if (!active) return;
 #pragma unroll
-  for (int n = 0; n < NT; ++n)
+  for (int rb = 0; rb < 2; ++rb) {
+    const int row = r0 + 32 * rb + l32;
+    if (row >= row_lim) continue;
+    const float l_row = l_part[rb] + shfl_xor_f(l_part[rb], 32);
+    const float inv = l_row > 0.f ? 1.0f / l_row : 0.f;
+    half_t* orow = Oh + (int64_t)row * p.o_ss;
 #pragma unroll
-    for (int q4 = 0; q4 < 4; ++q4) {
-      half4_t hv;
+    for (int n = 0; n < NT; ++n)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) hv[r] = (half_t)(oacc[n][4 * q4 + r] * inv);
-      *reinterpret_cast<half4_t*>(orow + 32 * n + 8 * q4 + 4 * g) = hv;
-    }
+      for (int q4 = 0; q4 < 4; ++q4) {
+        half4_t hv;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) hv[r] = (half_t)(oacc[rb][n][4 * q4 + r] * inv);
+        *reinterpret_cast<half4_t*>(orow + 32 * n + 8 * q4 + 4 * g) = hv;
+      }
+  }
 }
 
 template <int D, bool CAUSAL, bool VARLEN>
@@ -370,10 +389,11 @@ extern "C" int akt_prefill_fwd(const void* q, const void* k, const void* v, void
   p.Hkv = (int)num_kv_heads;
   p.G = (int)(num_q_heads / num_kv_heads);
   p.S = (int)seq_len;
-  p.n_qblk = (int)ceil_div(seq_len, kBM);
+  p.n_rb = (int)ceil_div(seq_len, kRows);
+  p.n_sg = (int)ceil_div((int64_t)p.G * p.n_rb, kSlots);
   p.xcd_map = ((batch * num_kv_heads) % 8 == 0) ? 1 : 0;
   p.qk_scale = softmax_scale * kLog2e;
-  const int64_t grid = batch * num_q_heads * p.n_qblk;
+  const int64_t grid = batch * num_kv_heads * p.n_sg;
   AKT_CHECK(grid < (1ll << 31), "problem too large");
   const bool is_causal = causal != 0;
   const bool is_var = varlen != nullptr;

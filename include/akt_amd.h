@@ -9,6 +9,12 @@
  * entry points take a caller-owned workspace of the size reported by the
  * matching *_workspace_size() function.
  *
+ * Workspace contract (all decode entry points): the first 256 bytes hold
+ * scheduling counters that must be zero before a workspace is first used;
+ * every call leaves them zero again when it completes.  A workspace may be
+ * reused by any decode entry point, but only by calls ordered on one stream
+ * (calls that overlap in time must use different workspaces).
+ *
  * Tensor element types: q/k/v/o and KV pools are IEEE fp16; page tables,
  * kept-token indices and counts are int32; MagicPIG K/L and LSE are fp32.
  * Strides are in elements.  The innermost (head_dim) stride must be 1 and
@@ -77,7 +83,9 @@ int akt_prefill_fwd(const void* q, const void* k, const void* v, void* o,
  *   o: contiguous [batch, num_q_heads, head_dim] fp16;
  *   lse: optional contiguous [batch, num_q_heads] fp32 (natural log of the
  *   softmax normaliser of the scaled scores).  head_dim: 64, 128 or 256.
- *   chunk_tokens: split-KV chunk length (multiple of 64), 0 = automatic.
+ *   chunk_tokens: split-KV chunk length: 128, 256 or 512 tokens, 0 = automatic
+ *   (a hint: pages that do not hold whole 16-token groups, and paged batches
+ *   over 1024 sequences, use 256).
  */
 size_t akt_decode_workspace_size(int64_t batch, int64_t num_q_heads, int64_t num_kv_heads,
                                  int64_t seq_len, int64_t head_dim, int64_t chunk_tokens);

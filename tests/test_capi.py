@@ -83,9 +83,10 @@ def test_workspace_sizes_scale_with_problem():
     a = lib.akt_decode_paged_workspace_size(32, 32, 8, 128, 16, 8448, 0)
     b = lib.akt_decode_paged_workspace_size(32, 32, 8, 128, 16, 2 * 8448, 0)
     assert 0 < a <= b
-    assert lib.akt_decode_workspace_size(8, 64, 16, 1024, 64, 1024) == 0  # one chunk: no partials
-    assert lib.akt_sparse_decode_workspace_size(1, 32, 128, 3840, 1) == 0
-    assert lib.akt_sparse_decode_workspace_size(1, 32, 128, 3840, 8) == 32 * 8 * 132 * 4
+    # 256-byte counter header, plus partials only when a unit has several chunks
+    assert lib.akt_decode_workspace_size(8, 64, 16, 512, 64, 512) == 256
+    assert lib.akt_sparse_decode_workspace_size(1, 32, 128, 3840, 1) == 256
+    assert lib.akt_sparse_decode_workspace_size(1, 32, 128, 3840, 8) == 256 + 32 * 8 * 132 * 4
 
 
 def test_kept_index_rejects_short_row_stride():

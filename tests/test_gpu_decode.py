@@ -36,7 +36,7 @@ def test_decode_shapes(dev, D, G, S):
     assert_close(lse, rl, atol=1e-4, what="decode lse")
 
 
-@pytest.mark.parametrize("chunk", [64, 128, 192, 4096])
+@pytest.mark.parametrize("chunk", [128, 256, 512])
 def test_decode_chunking_does_not_change_results(dev, chunk):
     q, K, V = _dec_inputs(3, 2, 4, 4, 777, 128)
     o, lse = _ops.decode(q.to(dev), K.to(dev), V.to(dev), 0.09, return_lse=True,
@@ -159,3 +159,16 @@ def test_paged_invalid_page_ids_are_skipped(dev):
     ro, _ = naive.naive_paged_attention(q, pool, torch.tensor([0, 2], dtype=torch.int32), good,
                                         torch.tensor([16], dtype=torch.int32))
     assert_close(o, ro, what="invalid page skipped")
+
+
+def test_paged_repeated_calls_are_bit_identical(dev):
+    """Dynamic work scheduling changes which workgroup runs a chunk, never the result;
+    the scheduling counters are left at zero by every call."""
+    p = syn.paged_config(B=16, min_len=256, max_len=6000).to(dev)
+    outs = [pg.flash_attention_decode_paged(p.q, p.pool, p.indptr, p.indices, p.last_len)
+            for _ in range(4)]
+    for o in outs[1:]:
+        assert torch.equal(o, outs[0])
+    from attention_kernel_triton_amd import _native
+    for buf in _native._WS_CACHE.values():
+        assert int(buf[:256].count_nonzero()) == 0
