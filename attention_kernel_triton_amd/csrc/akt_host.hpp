@@ -2,6 +2,7 @@
 // message, argument checks and launch-status translation.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdarg.h>
 #include <stdint.h>
@@ -19,18 +20,30 @@ void clear_error();
 // Returns AKT_ERR_HIP with a message if the last launch on this thread failed.
 int check_launch(const char* what);
 
-// Records a HIP event pair around a kernel launch while the kernel timer is
-// enabled (akt_kernel_timer_enable); a no-op otherwise.
+// Launches a kernel; while the kernel timer is enabled
+// (akt_kernel_timer_enable) the launch goes through hipExtLaunchKernel with an
+// event pair that the runtime stamps with the dispatch's own start and end
+// times, so the timer sees kernel execution only (no queueing or launch gaps).
 class KernelTimer {
  public:
-  explicit KernelTimer(void* stream);
+  KernelTimer();
   ~KernelTimer();
   KernelTimer(const KernelTimer&) = delete;
   KernelTimer& operator=(const KernelTimer&) = delete;
-  void stop();
+
+  template <typename... Args, typename F = void (*)(Args...)>
+  void launch(F kernel, dim3 grid, dim3 block, uint32_t lds_bytes, hipStream_t stream,
+              Args... args) {
+    if (armed_) {
+      hipExtLaunchKernelGGL(kernel, grid, block, lds_bytes, stream, start_, stop_, 0, args...);
+      commit();
+    } else {
+      hipLaunchKernelGGL(kernel, grid, block, lds_bytes, stream, args...);
+    }
+  }
 
  private:
-  void* stream_;
+  void commit();
   hipEvent_t start_ = nullptr, stop_ = nullptr;
   bool armed_ = false;
 };

@@ -28,26 +28,25 @@ int check_launch(const char* what) {
   return AKT_OK;
 }
 
-// Opt-in kernel timer: while enabled, every entry point records a HIP event
-// pair around its dominant kernel; akt_kernel_timer_read() waits for the
-// recorded pairs and returns their summed elapsed time.
+// Opt-in kernel timer: while enabled, every entry point's dominant kernel is
+// launched with an event pair stamped by the runtime at the dispatch's start
+// and end; akt_kernel_timer_read() waits for the recorded pairs and returns
+// their summed elapsed time.
 namespace {
 std::mutex g_timer_mu;
 bool g_timer_on = false;
 std::vector<std::pair<hipEvent_t, hipEvent_t>> g_timer_pairs;
 }  // namespace
 
-KernelTimer::KernelTimer(void* stream) : stream_(stream) {
+KernelTimer::KernelTimer() {
   std::lock_guard<std::mutex> lk(g_timer_mu);
   if (!g_timer_on) return;
   if (hipEventCreate(&start_) != hipSuccess || hipEventCreate(&stop_) != hipSuccess) return;
-  if (hipEventRecord(start_, (hipStream_t)stream_) == hipSuccess) armed_ = true;
+  armed_ = true;
 }
 
-void KernelTimer::stop() {
-  if (!armed_) return;
+void KernelTimer::commit() {
   armed_ = false;
-  if (hipEventRecord(stop_, (hipStream_t)stream_) != hipSuccess) return;
   std::lock_guard<std::mutex> lk(g_timer_mu);
   g_timer_pairs.emplace_back(start_, stop_);
   start_ = stop_ = nullptr;  // owned by g_timer_pairs now

@@ -968,9 +968,8 @@ int launch_split(const SplitParams& p, dim3 grid, hipStream_t st) {
     if (cap <= 0) return set_error(AKT_ERR_HIP, "occupancy query failed");
     grid = dim3((unsigned)(items < cap ? items : cap), 1);
   }
-  KernelTimer timer(st);
-  hipLaunchKernelGGL(kernel, grid, dim3(kThreads), 0, st, p);
-  timer.stop();
+  KernelTimer timer;
+  timer.launch(kernel, grid, dim3(kThreads), 0, st, p);
   return check_launch("split_kernel");
 }
 

@@ -82,17 +82,16 @@ int launch_kept(bool from_mask, const uint8_t* mask, const float* uniform, float
   if (rows == 0) return AKT_OK;
   AKT_CHECK(from_mask ? (mask || n == 0) : (uniform || n == 0), "input pointer is required");
   hipStream_t st = (hipStream_t)stream;
-  KernelTimer timer(st);
+  KernelTimer timer;
   if (from_mask) {
-    hipLaunchKernelGGL((kept_index_kernel<true>), dim3((unsigned)rows), dim3(kKThreads), 0, st,
-                       mask, nullptr, 0.f, n, row_stride, row_len, sparse_ind, l_max, sparse_nnz,
-                       ensure_nonempty);
+    timer.launch(kept_index_kernel<true>, dim3((unsigned)rows), dim3(kKThreads), 0, st, mask,
+                 (const float*)nullptr, 0.f, n, row_stride, row_len, sparse_ind, l_max,
+                 sparse_nnz, ensure_nonempty);
   } else {
-    hipLaunchKernelGGL((kept_index_kernel<false>), dim3((unsigned)rows), dim3(kKThreads), 0, st,
-                       nullptr, uniform, ratio, n, row_stride, row_len, sparse_ind, l_max,
-                       sparse_nnz, ensure_nonempty);
+    timer.launch(kept_index_kernel<false>, dim3((unsigned)rows), dim3(kKThreads), 0, st,
+                 (const uint8_t*)nullptr, uniform, ratio, n, row_stride, row_len, sparse_ind,
+                 l_max, sparse_nnz, ensure_nonempty);
   }
-  timer.stop();
   return check_launch("kept_index_kernel");
 }
 

@@ -332,9 +332,8 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(D == 
 
 template <int D, bool CAUSAL, bool VARLEN>
 int launch(const PrefillParams& p, unsigned grid, hipStream_t st) {
-  KernelTimer timer(st);
-  hipLaunchKernelGGL((prefill_kernel<D, CAUSAL, VARLEN>), dim3(grid), dim3(kPThreads), 0, st, p);
-  timer.stop();
+  KernelTimer timer;
+  timer.launch(prefill_kernel<D, CAUSAL, VARLEN>, dim3(grid), dim3(kPThreads), 0, st, p);
   return check_launch("prefill_kernel");
 }
 

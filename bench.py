@@ -10,8 +10,10 @@ Headline metric: paged decode HBM GB/s + prefill TFLOP/s.
 A step is one call of the drop-in entry point on the synthetic batch.  Each
 leg carries a roofline object for its dominant kernel (split-KV decode kernel,
 prefill kernel): algorithmic bytes (FLOPs) per launch / the kernel's mean
-duration from HIP events recorded around it on its launch stream, against
-MI355X's published peak (8 TB/s HBM, 2.5 PFLOP/s dense fp16).  The CPU
+duration from a HIP event pair that the runtime stamps with the dispatch's own
+start and end (hipExtLaunchKernel on the launch stream), against MI355X's
+published peak (8 TB/s HBM, 2.5 PFLOP/s dense fp16).  `traffic` is the HBM
+bytes per launch from the committed rocprofv3 counter summary in profiles/.  The CPU
 baseline is the repository's CPU restatement of the reference's naive path
 (oracle/, fp32) timed on a bounded sample on this host.
 
@@ -28,6 +30,25 @@ import time
 
 HBM_PEAK_GBS = 8000.0
 FP16_PEAK_TFLOPS = 2500.0
+PROFILES = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles")
+
+
+def _traffic(summary):
+    """HBM bytes per launch of a kernel, from its committed counter summary.
+
+    The summary records two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) of
+    this script, scaled by what the counters read for a device copy of known
+    size; it holds one line ``traffic_bytes_per_launch = N``.  None if absent.
+    """
+    path = os.path.join(PROFILES, summary)
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch"):
+                    return float(line.split("=")[1])
+    except OSError:
+        pass
+    return None
 
 
 def _parse():
@@ -101,7 +122,8 @@ def bench_paged(args):
         "bytes_per_step": nbytes,
         "roofline": {"bound": "hbm", "achieved": nbytes / t_kern / 1e9, "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": nbytes / t_kern / 1e9 / HBM_PEAK_GBS,
-                     "traffic": None, "kernel": "split_kernel<128,4,kModePaged>",
+                     "traffic": _traffic("split_kernel_paged_decode_config3.md"),
+                     "kernel": "split_kernel<128,4,kModePaged>",
                      "kernel_us": t_kern * 1e6},
         "tokens": sum(cfg.lens),
     }
@@ -142,7 +164,8 @@ def bench_prefill(args):
         "flops_per_step": flops,
         "roofline": {"bound": "mfma", "achieved": flops / t_kern / 1e12, "peak": FP16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": flops / t_kern / 1e12 / FP16_PEAK_TFLOPS,
-                     "traffic": None, "kernel": "prefill_kernel<64,causal>",
+                     "traffic": _traffic("prefill_kernel_causal_config0.md"),
+                     "kernel": "prefill_kernel<64,causal>",
                      "kernel_us": t_kern * 1e6},
     }
     if not args.no_cpu_baseline:
