@@ -50,20 +50,45 @@ __device__ __forceinline__ uint32_t shfl_u(uint32_t v, int src) {
   return (uint32_t)__shfl((int)v, src, kWave);
 }
 
+// Exchange with lane l ^ 32 / l ^ 16 through v_permlane32_swap /
+// v_permlane16_swap (no LDS round trip).  Swapping a register with itself
+// yields, in each lane, the pair {x[l], x[l ^ 32]} (or x[l ^ 16]) in some
+// order, so any commutative combine of the two results is the butterfly.
+__device__ __forceinline__ void swap32(float v, float& a, float& b) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  a = __uint_as_float(r[0]);
+  b = __uint_as_float(r[1]);
+}
+__device__ __forceinline__ void swap16(float v, float& a, float& b) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  a = __uint_as_float(r[0]);
+  b = __uint_as_float(r[1]);
+}
+
 // Max / sum over the two 32-lane halves of the wave (lane l and l ^ 32).
 __device__ __forceinline__ float xor32_max(float v) {
-  return fmaxf(v, shfl_xor_f(v, 32));
+  float a, b;
+  swap32(v, a, b);
+  return fmaxf(a, b);
 }
-__device__ __forceinline__ float xor32_sum(float v) { return v + shfl_xor_f(v, 32); }
+__device__ __forceinline__ float xor32_sum(float v) {
+  float a, b;
+  swap32(v, a, b);
+  return a + b;
+}
 
 // Reduce across the four 16-lane rows (l ^ 16, l ^ 32).
 __device__ __forceinline__ float rows_max(float v) {
-  v = fmaxf(v, shfl_xor_f(v, 16));
-  return fmaxf(v, shfl_xor_f(v, 32));
+  float a, b;
+  swap16(v, a, b);
+  return xor32_max(fmaxf(a, b));
 }
 __device__ __forceinline__ float rows_sum(float v) {
-  v += shfl_xor_f(v, 16);
-  return v + shfl_xor_f(v, 32);
+  float a, b;
+  swap16(v, a, b);
+  return xor32_sum(a + b);
 }
 
 // ---------------------------------------------------------------------------

@@ -13,25 +13,41 @@
 // causal extents.  Each wave owns 64 query rows as two 32-row MFMA blocks that
 // share every K and V fragment read from LDS.
 //
-// Per 64-key tile, staged row-major in LDS (sK, sV, rows padded by 16 bytes):
-//   S^T = K . Q^T    A = K rows from LDS (16-byte reads), B = Q^T in registers
-//   O^T = V^T . P^T  A = V^T via ds_read_b64_tr_b16 from the row-major V tile,
-//                    B = P^T taken straight from the S^T registers
-// Computing both products transposed makes each lane own one query row (lane &
-// 31) of each 32-row block; the two 32-lane halves hold complementary key (or
-// dim) slots, so row max / sum need one exchange between lane l and l ^ 32.
+// K/V staging.  Each 64-key tile of K and V goes global -> registers -> one
+// of four LDS tile buffers: while tile j is computed, tile j + 1 is already
+// published, tile j + 2 is being written and tile j + 3 is in flight from
+// HBM, and one barrier per tile both publishes a tile and retires tile j - 2's
+// buffer.  (Direct global -> LDS copies would be waited for before every
+// transposing LDS read, which defeats the prefetch.)  Rows are stored without
+// padding; 16-byte chunk c of row r sits at chunk position c ^ swz(r), which
+// keeps both the 16-byte K reads (8 consecutive rows, one chunk) and the
+// transposing V reads (4 rows x 2 chunks per 16 lanes) free of bank
+// conflicts.  Rows past the keys a tile may use are loaded from row 0 of the
+// sequence, so every staged value is finite and in bounds.
+//
+// Per 32-key step t a wave runs, with no dependence between the three parts:
+//   O^T += V^T . P(t-1)^T   A = V^T via ds_read_b64_tr_b16, B = the previous
+//                           step's probabilities straight from registers
+//   S(t+1)^T = K . Q^T      A = K rows (16-byte LDS reads), B = Q^T in registers
+//   softmax of S(t)^T       VALU / transcendental work
+// so the MFMA pipe and the VALU work of one wave overlap.  Computing both
+// products transposed makes each lane own one query row (lane & 31) of each
+// 32-row block; the two 32-lane halves hold complementary key (or dim) slots,
+// so row max / sum need one v_permlane32_swap.
 //
 // Softmax.  Scores are scaled by softmax_scale * log2(e) and exponentiated with
-// v_exp_f32, 32 keys at a time.  The running max is only raised when a tile's
-// max exceeds it by more than kRescaleSlack (log2 units); otherwise the stale
-// max is kept, which bounds P by 2^kRescaleSlack and skips the O rescale.  P is
-// rounded to fp16 for P.V (as the reference does at prefill_flash_attention.py:94)
-// and the normaliser sums the same rounded values.
+// v_exp_f32.  The running max is only raised when a step's max exceeds it by
+// more than kRescaleSlack (log2 units); otherwise the stale max is kept, which
+// bounds P by 2^kRescaleSlack and skips the O rescale.  A raise rescales the
+// normaliser at once and O after the step's P.V(t-1) has been accumulated.  P
+// is rounded to fp16 for P.V (as the reference does at
+// prefill_flash_attention.py:94) and the normaliser sums the same rounded values.
 //
 // Masking uses a select (score = -inf), not the reference's additive -1e6
 // (prefill_flash_attention.py:76), so non-finite padding never leaks.  In
-// var-len causal mode the K/V rows at or beyond a sequence's length are staged
-// as zeros, so padding cannot reach valid rows through P.V either.
+// var-len causal mode the K/V rows at or beyond a sequence's length are never
+// staged (row 0 is loaded in their place), so padding cannot reach valid rows
+// through P.V either.
 #include <math.h>
 
 #include "akt_common.hpp"
@@ -45,6 +61,7 @@ constexpr int kPThreads = 256;
 constexpr int kSlots = 4;   // waves per workgroup
 constexpr int kRows = 64;   // query rows per slot (two 32-row MFMA blocks)
 constexpr int kBN = 64;     // keys per staged tile
+constexpr int kNBuf = 4;    // LDS tile buffers
 constexpr float kRescaleSlack = 8.0f;
 #define AKT_P_NEG_INF (-__builtin_inff())
 
@@ -73,10 +90,15 @@ typedef __attribute__((address_space(3))) short4_t lds_short4;
 // component (i % 4) of the 8-byte chunk addressed by source lane 4j + i / 4.
 // If source lane s addresses row k0 + s / 4, columns c0 + 4 (s % 4) .. +3 of a
 // row-major fp16 matrix, output lane i receives rows k0..k0+3 of column c0 + i.
-__device__ __forceinline__ uint2 ds_read_tr16(const half_t* lds_ptr) {
+__device__ __forceinline__ uint2 ds_read_tr16(const char* lds_ptr) {
   const short4_t r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4*)(lds_ptr));
   return __builtin_bit_cast(uint2, r);
 }
+
+// Chunk-position swizzle of a tile row (see the header comment).  Any 8
+// consecutive rows get distinct values, and rows 4i..4i+3 get values that
+// differ in bits 1..2.
+__device__ __forceinline__ int swz(int r) { return ((r & 3) << 1) | ((r >> 2) & 1); }
 
 // Workgroup -> (batch, kv head, slot group).  Causal work is issued heaviest
 // slot group first; with xcd_map the workgroups of one kv head land on one
@@ -102,17 +124,18 @@ __device__ __forceinline__ void map_block(const PrefillParams& p, bool causal, i
 }
 
 template <int D, bool CAUSAL, bool VARLEN>
-__global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(D == 64 ? 2 : 1, 2))) void prefill_kernel(PrefillParams p) {
-  constexpr int KS = D / 16;       // MFMA k-steps over the head dim
-  constexpr int HALF = D / 2;      // head dims per lane half in S^T operands
-  constexpr int ROW = D + 8;       // sK / sV row pitch (halfs)
-  constexpr int NT = D / 32;       // 32-dim output tiles
-  constexpr int CHUNKS = kBN * D / 8;  // 16-byte chunks per K (or V) tile
-  constexpr int PER_T = CHUNKS / kPThreads;
-  static_assert(CHUNKS % kPThreads == 0, "tile split");
+__global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(D == 64 ? 2 : 1, 2)))
+void prefill_kernel(PrefillParams p) {
+  constexpr int KS = D / 16;              // MFMA k-steps over the head dim
+  constexpr int HALF = D / 2;             // head dims per lane half in S^T operands
+  constexpr int NT = D / 32;              // 32-dim output tiles
+  constexpr int CPR = D / 8;              // 16-byte chunks per K/V row
+  constexpr int ROWB = D * 2;             // bytes per K/V row
+  constexpr int TILEB = kBN * ROWB;       // bytes per K (or V) tile
+  constexpr int BUFB = 2 * TILEB;         // bytes per tile buffer (K then V)
+  static_assert((kBN * CPR) % kPThreads == 0, "tile split");
 
-  __shared__ __attribute__((aligned(16))) half_t sK[kBN * ROW];
-  __shared__ __attribute__((aligned(16))) half_t sV[kBN * ROW];
+  __shared__ __attribute__((aligned(16))) char lds[kNBuf * BUFB];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -147,10 +170,14 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(D == 
     }
     kv_end = min(row_lim, last_r0 + kRows);
   }
-  const int key_lim = (VARLEN && CAUSAL) ? len : S;  // keys at or past this are staged as zeros
-  const int n_tiles = (kv_end + kBN - 1) / kBN;
-  const int wave_kv_end = CAUSAL ? min(kv_end, r0 + kRows) : kv_end;
+  const int key_lim = (VARLEN && CAUSAL) ? len : S;  // rows at or past this are never staged
+  const int n_tiles = uniform((kv_end + kBN - 1) / kBN);
   if (n_tiles == 0) return;
+  const int wave_kv_end = CAUSAL ? min(kv_end, r0 + kRows) : kv_end;
+  // 32-key steps of this wave, rounded up to a pair.  A padding step covers
+  // keys at or past the wave's range: they are masked (past S or past every
+  // row of the wave) and lie in the last staged tile, so they contribute zero.
+  const int n_h = uniform(active ? 2 * ((wave_kv_end + 63) / 64) : 0);
 
   const int h = kvh * p.G + hl;
   const half_t* __restrict__ Qh = p.q + (int64_t)b * p.q_sb + (int64_t)h * p.q_sh;
@@ -158,7 +185,50 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(D == 
   const half_t* __restrict__ Vh = p.v + (int64_t)b * p.v_sb + (int64_t)kvh * p.v_sh;
   half_t* __restrict__ Oh = p.o + (int64_t)b * p.o_sb + (int64_t)h * p.o_sh;
 
-  // Q^T fragments of the two 32-row blocks: lane -> row, dims g*HALF + 8s + e.
+  // ---- K/V tile staging through registers: chunk i of this thread is
+  // 16-byte chunk tid + 256 i of the K (then V) tile: row st_r[i], global
+  // chunk st_c[i], stored at chunk position st_c[i] ^ swz(row).
+  constexpr int PER_T = kBN * CPR / kPThreads;  // chunks per thread per matrix
+  uint4_t kst[PER_T], vst[PER_T];
+  auto load_tile = [&](int j) {
+#pragma unroll
+    for (int i = 0; i < PER_T; ++i) {
+      const int q = tid + i * kPThreads;
+      const int r = q / CPR, cc = q % CPR;
+      int key = j * kBN + r;
+      if (key >= key_lim) key = 0;
+      kst[i] = ld16(Kh + (int64_t)key * p.k_ss + 8 * cc);
+      vst[i] = ld16(Vh + (int64_t)key * p.v_ss + 8 * cc);
+    }
+  };
+  auto store_tile = [&](int j) {
+    char* buf = lds + (j % kNBuf) * BUFB;
+#pragma unroll
+    for (int i = 0; i < PER_T; ++i) {
+      const int q = tid + i * kPThreads;
+      const int r = q / CPR, cc = q % CPR;
+      const int off = r * ROWB + ((cc ^ swz(r)) * 16);
+      *reinterpret_cast<uint4_t*>(buf + off) = kst[i];
+      *reinterpret_cast<uint4_t*>(buf + TILEB + off) = vst[i];
+    }
+  };
+
+  // ---- per-lane LDS byte offsets (within a tile buffer) of the fragments
+  // K rows for S^T: key l32 of the step, chunks g * HALF / 8 + s.
+  int koff[KS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) koff[s] = l32 * ROWB + (((g * HALF / 8) + s) ^ swz(l32)) * 16;
+  // V^T via tr16: source lane s16 addresses key 4g + s16 / 4 of each 16-key
+  // block and dims 32n + 16 * ((lane >> 4) & 1) + 4 * (s16 % 4).
+  const int s16 = lane & 15;
+  const int vrow = 4 * g + (s16 >> 2);
+  const int vcl = 2 * ((lane >> 4) & 1) + ((s16 & 3) >> 1);
+  int voff[NT];
+#pragma unroll
+  for (int n = 0; n < NT; ++n)
+    voff[n] = TILEB + vrow * ROWB + (((4 * n + vcl) ^ swz(vrow)) * 16) + (s16 & 1) * 8;
+
+  // ---- Q^T fragments of the two 32-row blocks: lane -> row, dims g*HALF + 8s + e.
   half8_t qf[2][KS];
 #pragma unroll
   for (int rb = 0; rb < 2; ++rb) {
@@ -182,131 +252,177 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(D == 
   float l_part[2] = {0.f, 0.f};
   const float c = p.qk_scale;
   const uint32_t kOnes = 0x3c003c00u;
-
-  // Staging registers for the next tile (row-major 16-byte chunks).
-  uint4_t kst[PER_T], vst[PER_T];
-  auto load_tile = [&](int j) {
-    const int kbase = j * kBN;
+  // Per-lane causal / length limit: element r of a step's S^T holds key
+  // kh0 + 8 (r / 4) + 4 g + r % 4 of row r0 + 32 rb + l32.
+  int lim_base[2];
 #pragma unroll
-    for (int i = 0; i < PER_T; ++i) {
-      const int cidx = tid + i * kPThreads;
-      const int key = cidx / (D / 8);
-      const int dc = cidx - key * (D / 8);
-      const int kg = kbase + key;
-      const bool ok = kg < key_lim;
-      kst[i] = ok ? ld16(Kh + (int64_t)kg * p.k_ss + 8 * dc) : uint4_t{0, 0, 0, 0};
-      vst[i] = ok ? ld16(Vh + (int64_t)kg * p.v_ss + 8 * dc) : uint4_t{0, 0, 0, 0};
-    }
+  for (int rb = 0; rb < 2; ++rb) {
+    const int row = r0 + 32 * rb + l32;
+    lim_base[rb] = (CAUSAL ? min(row, S - 1) : S - 1) - 4 * g;
+  }
+
+  float16_t sA[2], sB[2];
+  uint32_t pA[2][8], pB[2][8];
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) pA[rb][i] = pB[rb][i] = 0u;
+
+  // Fragment reads of 32-key step t (its tile must be published).
+  auto load_kf = [&](int t, half8_t (&kf)[KS]) {
+    const char* kb = lds + ((t >> 1) % kNBuf) * BUFB + (t & 1) * 32 * ROWB;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) kf[s] = as_half8(*reinterpret_cast<const uint4_t*>(kb + koff[s]));
   };
-  auto store_tile = [&]() {
+  auto load_vf = [&](int t, half8_t (&vf)[2][NT]) {
+    const char* vb = lds + ((t >> 1) % kNBuf) * BUFB + (t & 1) * 32 * ROWB;
 #pragma unroll
-    for (int i = 0; i < PER_T; ++i) {
-      const int cidx = tid + i * kPThreads;
-      const int key = cidx / (D / 8);
-      const int dc = cidx - key * (D / 8);
-      *reinterpret_cast<uint4_t*>(&sK[key * ROW + 8 * dc]) = kst[i];
-      *reinterpret_cast<uint4_t*>(&sV[key * ROW + 8 * dc]) = vst[i];
-    }
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int n = 0; n < NT; ++n) {
+        const char* vp = vb + voff[n] + u * 16 * ROWB;
+        const uint2 lo = ds_read_tr16(vp);
+        const uint2 hi = ds_read_tr16(vp + 8 * ROWB);
+        vf[u][n] = as_half8(uint4_t{lo.x, lo.y, hi.x, hi.y});
+      }
   };
-
-  // V^T fragment addresses: lane l's 16-lane group reads dims d0 + (0..15)
-  // for keys k0..k0+3; source lane s = l % 16 addresses key k0 + s / 4,
-  // dims d0 + 4 (s % 4).
-  const int s16 = lane & 15;
-  const int vt_dim = 16 * ((lane >> 4) & 1) + 4 * (s16 & 3);
-  const int vt_key = s16 >> 2;
-
-  load_tile(0);
-  for (int j = 0; j < n_tiles; ++j) {
-    __syncthreads();
-    store_tile();
-    __syncthreads();
-    if (j + 1 < n_tiles) load_tile(j + 1);
-
-    const int kt0 = j * kBN;
-    if (!active || kt0 >= wave_kv_end) continue;  // wave-uniform
-
+  // S^T = K . Q^T for one step.
+  auto qk_mfma = [&](const half8_t (&kf)[KS], float16_t (&sdst)[2]) {
 #pragma unroll
-    for (int hf = 0; hf < 2; ++hf) {
-      const int kh0 = kt0 + 32 * hf;
-      if (kh0 >= wave_kv_end) break;  // wave-uniform: the rest of the tile is masked
-
-      // ---- S^T = K . Q^T for 32 keys x (2 x 32 rows) ------------------------
-      float16_t sacc[2];
+    for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) sdst[rb][r] = 0.f;
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+#pragma unroll
+      for (int rb = 0; rb < 2; ++rb) sdst[rb] = mfma32x32x16(kf[s], qf[rb][s], sdst[rb]);
+  };
+  // O^T += V^T . P^T for one step.
+  auto pv_mfma = [&](const half8_t (&vf)[2][NT], const uint32_t (&pk)[2][8]) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      half8_t bop[2];
 #pragma unroll
       for (int rb = 0; rb < 2; ++rb)
+        bop[rb] = as_half8(uint4_t{pk[rb][4 * u], pk[rb][4 * u + 1], pk[rb][4 * u + 2],
+                                   pk[rb][4 * u + 3]});
 #pragma unroll
-        for (int r = 0; r < 16; ++r) sacc[rb][r] = 0.f;
-      const half_t* kr = &sK[(32 * hf + l32) * ROW + g * HALF];
+      for (int n = 0; n < NT; ++n)
 #pragma unroll
-      for (int s = 0; s < KS; ++s) {
-        const half8_t a = as_half8(*reinterpret_cast<const uint4_t*>(kr + 8 * s));
-#pragma unroll
-        for (int rb = 0; rb < 2; ++rb) sacc[rb] = mfma32x32x16(a, qf[rb][s], sacc[rb]);
-      }
-
-      // ---- mask ---------------------------------------------------------------
-      const bool need_mask = (CAUSAL && kh0 + 31 > r0) || (kh0 + 32 > S);
-      if (need_mask) {
-#pragma unroll
-        for (int rb = 0; rb < 2; ++rb) {
-          const int row = r0 + 32 * rb + l32;
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int key = kh0 + 8 * (r >> 2) + 4 * g + (r & 3);
-            const bool ok = (key < S) && (!CAUSAL || key <= row);
-            if (!ok) sacc[rb][r] = AKT_P_NEG_INF;
-          }
-        }
-      }
-
-      // ---- online softmax per 32-row block (row = l32) -------------------------
-      uint32_t pk[2][8];
+        for (int rb = 0; rb < 2; ++rb) oacc[rb][n] = mfma32x32x16(vf[u][n], bop[rb], oacc[rb][n]);
+    }
+  };
+  auto qk = [&](int t, float16_t (&sdst)[2]) {
+    half8_t kf[KS];
+    load_kf(t, kf);
+    qk_mfma(kf, sdst);
+  };
+  auto pv = [&](int t, const uint32_t (&pk)[2][8]) {
+    half8_t vf[2][NT];
+    load_vf(t, vf);
+    pv_mfma(vf, pk);
+  };
+  // One pipeline step t < n_h: mask S(t); then, in one scheduling region,
+  // the fragment reads, the max of S(t), P.V(t-1), S(t+1) and exp of S(t) --
+  // the MFMAs and the softmax VALU work are independent, so the scheduler can
+  // interleave them and keep both pipes busy; then the rare O / normaliser
+  // rescale, applied after P.V(t-1) (computed on the old max) has been
+  // accumulated.
+  auto step = [&](int t, float16_t (&scur)[2], float16_t (&snext)[2],
+                  const uint32_t (&pprev)[2][8], uint32_t (&pcur)[2][8]) {
+    const int kh0 = t * 32;
+    if ((CAUSAL && kh0 + 31 > r0) || kh0 + 32 > S) {  // wave-uniform
 #pragma unroll
       for (int rb = 0; rb < 2; ++rb) {
-        float mx = sacc[rb][0];
+        const int lim = lim_base[rb] - kh0;
 #pragma unroll
-        for (int r = 1; r < 16; ++r) mx = fmaxf(mx, sacc[rb][r]);
-        mx = fmaxf(mx, shfl_xor_f(mx, 32)) * c;
-        if (__any(mx > m_run[rb] + kRescaleSlack)) {
-          const float m_new = fmaxf(m_run[rb], mx);
-          const float alpha = (m_new > m_run[rb]) ? fast_exp2(m_run[rb] - m_new) : 1.0f;
-          l_part[rb] *= alpha;
-#pragma unroll
-          for (int n = 0; n < NT; ++n)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) oacc[rb][n][r] *= alpha;
-          m_run[rb] = m_new;
-        }
-        const float m_use = (m_run[rb] == AKT_P_NEG_INF) ? 0.f : m_run[rb];
-#pragma unroll
-        for (int r = 0; r < 16; r += 2) {
-          const float p0 = fast_exp2(__builtin_fmaf(sacc[rb][r], c, -m_use));
-          const float p1 = fast_exp2(__builtin_fmaf(sacc[rb][r + 1], c, -m_use));
-          pk[rb][r >> 1] = pack_half2(p0, p1);
-          l_part[rb] = dot2(pk[rb][r >> 1], kOnes, l_part[rb]);
-        }
+        for (int r = 0; r < 16; ++r)
+          if (8 * (r >> 2) + (r & 3) > lim) scur[rb][r] = AKT_P_NEG_INF;
       }
+    }
+    half8_t vf[2][NT], kf[KS];
+    load_vf(t > 0 ? t - 1 : 0, vf);
+    load_kf(t + 1, kf);
 
-      // ---- O^T += V^T . P^T over the 32 keys (two 16-key k-steps) -------------
+    // Every row has a valid key in step 0 (key 0: causal rows are >= 0 and
+    // S >= 1), so the running max is finite from step 0 on and needs no -inf
+    // guard.  IEEE maximum (NaN-propagating) needs no operand canonicalisation.
+    float m_new[2];
+    bool need_any = false;
 #pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        half8_t bop[2];
+    for (int rb = 0; rb < 2; ++rb) {
+      float mx = scur[rb][0];
 #pragma unroll
-        for (int rb = 0; rb < 2; ++rb)
-          bop[rb] = as_half8(uint4_t{pk[rb][4 * u], pk[rb][4 * u + 1], pk[rb][4 * u + 2],
-                                     pk[rb][4 * u + 3]});
-        const int k0 = 32 * hf + 16 * u + 4 * g + vt_key;
+      for (int r = 1; r < 16; ++r) mx = __builtin_elementwise_maximum(mx, scur[rb][r]);
+      float a, b;
+      swap32(mx, a, b);
+      mx = __builtin_elementwise_maximum(a, b) * c;
+      const bool need = mx > m_run[rb] + kRescaleSlack;
+      m_new[rb] = need ? mx : m_run[rb];
+      need_any |= need;
+    }
+    const bool rescale = __any(need_any);
+
+    pv_mfma(vf, pprev);
+    qk_mfma(kf, snext);
+
+    float l_step[2];
 #pragma unroll
-        for (int n = 0; n < NT; ++n) {
-          const half_t* vp = &sV[k0 * ROW + 32 * n + vt_dim];
-          const uint2 lo = ds_read_tr16(vp);
-          const uint2 hi = ds_read_tr16(vp + 8 * ROW);
-          const half8_t a = as_half8(uint4_t{lo.x, lo.y, hi.x, hi.y});
+    for (int rb = 0; rb < 2; ++rb) {
+      l_step[rb] = 0.f;
 #pragma unroll
-          for (int rb = 0; rb < 2; ++rb) oacc[rb][n] = mfma32x32x16(a, bop[rb], oacc[rb][n]);
-        }
+      for (int r = 0; r < 16; r += 2) {
+        const float p0 = fast_exp2(__builtin_fmaf(scur[rb][r], c, -m_new[rb]));
+        const float p1 = fast_exp2(__builtin_fmaf(scur[rb][r + 1], c, -m_new[rb]));
+        pcur[rb][r >> 1] = pack_half2(p0, p1);
+        l_step[rb] = dot2(pcur[rb][r >> 1], kOnes, l_step[rb]);
       }
+    }
+    // Keep the exp phase ahead of the rescale branch: without a use here the
+    // compiler sinks it past the branch, away from the MFMAs it overlaps.
+    asm volatile("" ::"v"(l_step[0]), "v"(l_step[1]));
+
+    if (rescale) {  // wave-uniform, rare
+#pragma unroll
+      for (int rb = 0; rb < 2; ++rb) {
+        const float alpha = m_new[rb] > m_run[rb] ? fast_exp2(m_run[rb] - m_new[rb]) : 1.0f;
+        l_part[rb] *= alpha;
+        m_run[rb] = m_new[rb];
+#pragma unroll
+        for (int n = 0; n < NT; ++n)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) oacc[rb][n][r] *= alpha;
+      }
+    }
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) l_part[rb] += l_step[rb];
+  };
+
+  load_tile(0);
+  store_tile(0);
+  if (n_tiles > 1) {
+    load_tile(1);
+    store_tile(1);
+  }
+  if (n_tiles > 2) load_tile(2);
+  __syncthreads();
+  if (n_h > 0) qk(0, sA);
+  // Steps run in pairs (2j, 2j + 1), one pair per tile; n_h is even.  At the
+  // top of pair j: sA = S(2j) and pB = P(2j - 1) (zero for j = 0).  The last
+  // pair's S(2j + 2) is computed from whatever its buffer holds and never
+  // used; the pair is followed by the drain P.V(2j + 1).
+  for (int j = 0; j < n_tiles; ++j) {
+    // Publishes tile j + 1 (stored before the previous barrier) and retires
+    // the buffer of tile j - 2, which now takes tile j + 2 from the staging
+    // registers; tile j + 3 is then fetched into them.
+    __syncthreads();
+    if (j + 2 < n_tiles) store_tile(j + 2);
+    if (j + 3 < n_tiles) load_tile(j + 3);
+    const int t = 2 * j;
+    if (t < n_h) {  // wave-uniform
+      step(t, sA, sB, pB, pA);
+      step(t + 1, sB, sA, pA, pB);
+      if (t + 2 == n_h) pv(t + 1, pB);
     }
   }
 
@@ -315,7 +431,7 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(D == 
   for (int rb = 0; rb < 2; ++rb) {
     const int row = r0 + 32 * rb + l32;
     if (row >= row_lim) continue;
-    const float l_row = l_part[rb] + shfl_xor_f(l_part[rb], 32);
+    const float l_row = xor32_sum(l_part[rb]);
     const float inv = l_row > 0.f ? 1.0f / l_row : 0.f;
     half_t* orow = Oh + (int64_t)row * p.o_ss;
 #pragma unroll
