@@ -754,16 +754,17 @@ __global__ __launch_bounds__(kThreads) void split_kernel(SplitParams p) {
 // ---------------------------------------------------------------------------
 template <int D, int GT, int MODE>
 __global__ __launch_bounds__(kThreads) void split_combine_kernel(SplitParams p) {
-  // One workgroup merges the partials of one unit (GT heads x D dims).  All
-  // loads of a phase are independent of each other, so the workgroup keeps
-  // many of them in flight instead of walking the chunks one by one.
+  // One workgroup merges the partials of one unit (GT heads x D dims) in one
+  // global round trip for up to 8 * NG chunks: every thread first issues its
+  // partial-output loads and the workgroup copies the chunks' (m, l, e) rows
+  // to LDS; after one barrier each thread derives its head's max and
+  // normalisers from LDS and accumulates.  Only the final chunk-group
+  // reduction goes through LDS again.
   constexpr bool SPARSE = (MODE == kModeSparseDense || MODE == kModeSparsePaged);
   constexpr int NV = GT * D / 4;                          // float4 output vectors
-  constexpr int NG = NV >= kThreads ? 1 : kThreads / NV;  // chunk groups in phase 3
-  constexpr int CAP = 2048 / GT;                          // chunk weights kept in LDS
-  __shared__ float sm_w[CAP * GT];
-  __shared__ float sm_red[kThreads];
-  __shared__ float sm_M[GT], sm_L[GT], sm_E[GT];
+  constexpr int NG = NV >= kThreads ? 1 : kThreads / NV;  // chunk groups
+  constexpr int MLCAP = 1024 / GT;                        // chunk rows kept in LDS
+  __shared__ float4_t sm_ml[MLCAP * GT];
   __shared__ float4_t sm_o[NG > 1 ? kThreads : 1];
 
   const int tid = threadIdx.x;
@@ -807,10 +808,12 @@ __global__ __launch_bounds__(kThreads) void split_combine_kernel(SplitParams p) 
   auto ml = [&](int c, int h) -> float4_t {
     return *reinterpret_cast<const float4_t*>(p.part_ml + ((first + c * step) * GT + h) * 4);
   };
+  auto po = [&](int c, int h, int d0) -> float4_t {
+    return *reinterpret_cast<const float4_t*>(p.part_o + ((first + c * step) * GT + h) * D + d0);
+  };
 
-  // Phase 0: issue the first U chunk rows of partial outputs for this
-  // thread's float4 before anything else, so these loads overlap the
-  // (m, l, e) loads of phases 1-2 (one round trip instead of three).
+  // Round trip: partial outputs of the first U chunks of this thread's chunk
+  // group, and the (m, l, e) rows of up to MLCAP chunks into LDS.
   constexpr int U = 8;
   constexpr int VSTEP = kThreads / NG;  // output vectors per pass
   constexpr int NPASS = (NV + VSTEP - 1) / VSTEP;
@@ -822,84 +825,49 @@ __global__ __launch_bounds__(kThreads) void split_combine_kernel(SplitParams p) 
     const int h = (vec * 4) / D;
     const int d0 = vec * 4 - h * D;
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int c = max(0, min(cg + u * NG, nch - 1));
-      ov[ps][u] = *reinterpret_cast<const float4_t*>(
-          p.part_o + ((first + c * step) * GT + h) * D + d0);
-    }
+    for (int u = 0; u < U; ++u) ov[ps][u] = po(max(0, min(cg + u * NG, nch - 1)), h, d0);
   }
+  const int nml = min(nch, MLCAP);
+  for (int i = tid; i < nml * GT; i += kThreads) sm_ml[i] = ml(i / GT, i % GT);
+  __syncthreads();
+  auto mlrow = [&](int c, int h) -> float4_t { return c < MLCAP ? sm_ml[c * GT + h] : ml(c, h); };
 
-  // Phase 1: per-head max over chunks.  Thread t serves head t % GT.
-  const int h1 = tid % GT;
-  float mloc = AKT_NEG_INF;
-  for (int c = tid / GT; c < nch; c += kThreads / GT) mloc = fmaxf(mloc, ml(c, h1)[0]);
-  sm_red[tid] = mloc;
-  __syncthreads();
-  if (tid < GT) {
-    float M = AKT_NEG_INF;
-    for (int i = tid; i < kThreads; i += GT) M = fmaxf(M, sm_red[i]);
-    sm_M[tid] = M;
-  }
-  __syncthreads();
-
-  // Phase 2: chunk weights 2^(m_c - M) and the two normalisers.
-  const float M1 = sm_M[h1];
-  float lloc = 0.f, eloc = 0.f;
-  for (int c = tid / GT; c < nch; c += kThreads / GT) {
-    const float4_t v = ml(c, h1);
-    const float w = (M1 == AKT_NEG_INF) ? 0.f : fast_exp2(v[0] - M1);
-    if (c < CAP) sm_w[c * GT + h1] = w;
-    lloc += w * v[1];
-    eloc += w * v[2];
-  }
-  sm_red[tid] = lloc;
-  __syncthreads();
-  if (tid < GT) {
-    float L = 0.f;
-    for (int i = tid; i < kThreads; i += GT) L += sm_red[i];
-    sm_L[tid] = L;
-  }
-  __syncthreads();
-  sm_red[tid] = eloc;
-  __syncthreads();
-  if (tid < GT) {
-    float E = 0.f;
-    for (int i = tid; i < kThreads; i += GT) E += sm_red[i];
-    sm_E[tid] = E;
-  }
-  __syncthreads();
-
-  // Phase 3: weighted sum of the partial outputs (the first U chunk rows are
-  // already in registers), NG chunk groups reduced through LDS.
-  auto weight = [&](int c, int h, float Mh) -> float {
-    if (c < CAP) return sm_w[c * GT + h];
-    return (Mh == AKT_NEG_INF) ? 0.f : fast_exp2(ml(c, h)[0] - Mh);
-  };
 #pragma unroll
   for (int ps = 0; ps < NPASS; ++ps) {
     const int vec = ps * VSTEP + tid % VSTEP;
     const int h = (min(vec, NV - 1) * 4) / D;
     const int d0 = min(vec, NV - 1) * 4 - h * D;
-    const float Mh = sm_M[h];
+    // Head h's max and the two normalisers (every thread of the head computes
+    // the same values from broadcast LDS reads).
+    float M = AKT_NEG_INF;
+    for (int c = 0; c < nch; ++c) M = fmaxf(M, mlrow(c, h)[0]);
+    float L = 0.f, E = 0.f;
+    if (M != AKT_NEG_INF) {
+      for (int c = 0; c < nch; ++c) {
+        const float4_t v = mlrow(c, h);
+        const float w = fast_exp2(v[0] - M);
+        L += w * v[1];
+        E += w * v[2];
+      }
+    }
+    auto weight = [&](int c) -> float {
+      return M == AKT_NEG_INF ? 0.f : fast_exp2(mlrow(c, h)[0] - M);
+    };
     float4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int c = cg + u * NG;
-      if (c < nch) acc += weight(c, h, Mh) * ov[ps][u];
+      if (c < nch) acc += weight(c) * ov[ps][u];
     }
     // Remaining chunks in batches of U independent loads (one round trip each).
     for (int c0 = cg + U * NG; c0 < nch; c0 += U * NG) {
       float4_t ob[U];
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int c = min(c0 + u * NG, nch - 1);
-        ob[u] = *reinterpret_cast<const float4_t*>(
-            p.part_o + ((first + c * step) * GT + h) * D + d0);
-      }
+      for (int u = 0; u < U; ++u) ob[u] = po(min(c0 + u * NG, nch - 1), h, d0);
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int c = c0 + u * NG;
-        if (c < nch) acc += weight(c, h, Mh) * ob[u];
+        if (c < nch) acc += weight(c) * ob[u];
       }
     }
     if constexpr (NG > 1) {
@@ -911,17 +879,13 @@ __global__ __launch_bounds__(kThreads) void split_combine_kernel(SplitParams p) 
       __syncthreads();
     }
     if (cg == 0 && vec < NV && h < nh) {
-      const float L = sm_L[h];
       const float inv = L > 0.f ? 1.0f / L : 0.f;
       const int64_t row = (int64_t)b * p.Hq + hq0 + h;
       half4_t hv;
 #pragma unroll
       for (int r = 0; r < 4; ++r) hv[r] = (half_t)(acc[r] * inv);
       *reinterpret_cast<half4_t*>(p.o + row * D + d0) = hv;
-      if (d0 == 0 && p.lse) {
-        const float E = sm_E[h];
-        p.lse[row] = E > 0.f ? (sm_M[h] + log2f(E)) * kLn2 : AKT_NEG_INF;
-      }
+      if (d0 == 0 && p.lse) p.lse[row] = E > 0.f ? (M + log2f(E)) * kLn2 : AKT_NEG_INF;
     }
   }
 }
@@ -1035,8 +999,11 @@ int launch_d(int D, int gt, const SplitParams& p, dim3 grid, dim3 cgrid, hipStre
 
 // Automatic chunk length for dense / paged caches: the smallest supported
 // length (128, 256, 512) that keeps the item count near 4096.
+// Smallest supported chunk that cuts the launch into at most ~2048 items:
+// enough to balance a persistent grid of a few hundred workgroups, few enough
+// that the combine reads a handful of partials per unit.
 int64_t auto_chunk(int64_t total_tokens, int64_t units) {
-  const int64_t want = ceil_div(total_tokens * units, 4096);
+  const int64_t want = ceil_div(total_tokens * units, 2048);
   int64_t c = 128;
   while (c < want && c < kMaxChunk) c <<= 1;
   return c;

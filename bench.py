@@ -71,19 +71,26 @@ def _log(msg):
 
 
 def _time_steps(fn, steps, warmup):
-    """Wall time per step and mean dominant-kernel time (HIP events) per step."""
+    """Wall time per step, and mean dominant-kernel time per step.
+
+    The step time comes from a loop with nothing but the steps in it; the
+    kernel time from a second loop of the same steps in which the library
+    launches its dominant kernel with a HIP event pair stamped on the dispatch.
+    """
     import torch
     from attention_kernel_triton_amd import _native
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        fn()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
     with _native.kernel_timer() as kt:
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
         for _ in range(steps):
             fn()
         torch.cuda.synchronize()
-        wall = time.perf_counter() - t0
     if kt.launches != steps:
         raise RuntimeError(f"expected {steps} timed launches, got {kt.launches}")
     return wall / steps, kt.total_ms / 1e3 / steps
