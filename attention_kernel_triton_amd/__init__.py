@@ -12,6 +12,7 @@ Modules mirror the reference repository's files (KiritoHugh/attention_kernel_tri
   magicpig_sparsetoken_decode_flash_attention_redundant_var_len_paged_with_norm
                                                 magicpig_sparsetoken_flash_attention_decode_paged
   kept_index                                    select_kept (device kept-index selection)
+  merge_states                                  merge_states (LSE merge of partial results)
 
 All of them run hand-written HIP kernels from libakt_amd.so (built by
 ``python -m attention_kernel_triton_amd.build``) through its C ABI.
@@ -27,4 +28,5 @@ __all__ = [
     "sparsetoken_decode_flash_attention_redundant_var_len_paged",
     "magicpig_sparsetoken_decode_flash_attention_redundant_var_len_paged_with_norm",
     "kept_index",
+    "merge_states",
 ]

@@ -47,8 +47,12 @@ def _same_device(dev, **tensors) -> None:
 
 
 # --------------------------------------------------------------------------- prefill
-def prefill(Q, K, V, causal: bool, softmax_scale: float, varlen=None) -> torch.Tensor:
-    """O = softmax(scale * Q K^T [+ causal mask]) V for Q [B,Hq,S,D], K/V [B,Hkv,S,D]."""
+def prefill(Q, K, V, causal: bool, softmax_scale: float, varlen=None, return_lse: bool = False):
+    """O = softmax(scale * Q K^T [+ causal mask]) V for Q [B,Hq,S,D], K/V [B,Hkv,S,D].
+
+    With return_lse, also the fp32 natural-log normaliser [B, Hq, S] of every
+    computed row (rows a var-len call leaves unwritten stay uninitialised).
+    """
     Q = _half_rows("Q", Q)
     K = _half_rows("K", K)
     V = _half_rows("V", V)
@@ -65,12 +69,65 @@ def prefill(Q, K, V, causal: bool, softmax_scale: float, varlen=None) -> torch.T
         varlen = varlen.contiguous()
         vptr, vbits = N.ptr(varlen), (64 if varlen.dtype == torch.int64 else 32)
     lib = N.load()
+    if return_lse:
+        lse = torch.empty((B, H, S), dtype=torch.float32, device=Q.device)
+        rc = lib.akt_prefill_fwd_lse(N.ptr(Q), N.ptr(K), N.ptr(V), N.ptr(O), N.ptr(lse), B, H,
+                                     K.shape[1], S, D, N.strides(Q), N.strides(K), N.strides(V),
+                                     N.strides(O), N.strides(lse), float(softmax_scale),
+                                     1 if causal else 0, vptr, vbits, N.stream_of(Q))
+        N.check(rc, "akt_prefill_fwd_lse")
+        return O, lse
     rc = lib.akt_prefill_fwd(N.ptr(Q), N.ptr(K), N.ptr(V), N.ptr(O), B, H, K.shape[1], S, D,
                              N.strides(Q), N.strides(K), N.strides(V), N.strides(O),
                              float(softmax_scale), 1 if causal else 0, vptr, vbits,
                              N.stream_of(Q))
     N.check(rc, "akt_prefill_fwd")
     return O
+
+
+# --------------------------------------------------------------------------- merge
+_DTYPE_CODE = {torch.float16: 0, torch.float32: 1}
+
+
+def merge_states(o, lse, out_dtype=None):
+    """Log-sum-exp merge of N partial attention states.
+
+    o: [N, ..., D] fp16 or fp32 partial outputs over disjoint key sets;
+    lse: [N, ...] fp32 natural-log normalisers.  Returns (o_merged [..., D]
+    in out_dtype (default o's dtype), lse_merged [...] fp32).
+    """
+    _need_gpu("o", o)
+    _need_gpu("lse", lse)
+    _same_device(o.device, lse=lse)
+    if o.dtype not in _DTYPE_CODE:
+        raise TypeError(f"o must be float16 or float32, got {o.dtype}")
+    if lse.dtype != torch.float32:
+        raise TypeError(f"lse must be float32, got {lse.dtype}")
+    if o.dim() < 2 or tuple(lse.shape) != tuple(o.shape[:-1]):
+        raise ValueError(f"lse shape {tuple(lse.shape)} must equal o.shape[:-1] = "
+                         f"{tuple(o.shape[:-1])}")
+    out_dtype = o.dtype if out_dtype is None else out_dtype
+    if out_dtype not in _DTYPE_CODE:
+        raise TypeError(f"out_dtype must be float16 or float32, got {out_dtype}")
+    n, D = o.shape[0], o.shape[-1]
+    rest = tuple(o.shape[1:-1])
+    rows = 1
+    for r in rest:
+        rows *= r
+    o3 = o.reshape(n, rows, D)
+    esz = o.element_size()
+    if (o3.stride(-1) != 1 or o3.data_ptr() % 16 or any((s * esz) % 16 for s in o3.stride()[:2])):
+        o3 = o3.contiguous()
+    l2 = lse.reshape(n, rows)
+    out = torch.empty(rest + (D,), dtype=out_dtype, device=o.device)
+    lse_out = torch.empty(rest, dtype=torch.float32, device=o.device)
+    lib = N.load()
+    rc = lib.akt_merge_states(N.ptr(o3), _DTYPE_CODE[o.dtype], N.ptr(l2), N.ptr(out),
+                              _DTYPE_CODE[out_dtype], N.ptr(lse_out), n, rows, D,
+                              N.i64s(o3.stride(0), o3.stride(1)), N.i64s(l2.stride(0), l2.stride(1)),
+                              D, 1, N.stream_of(o))
+    N.check(rc, "akt_merge_states")
+    return out, lse_out
 
 
 # --------------------------------------------------------------------------- decode

@@ -49,6 +49,7 @@ class KernelTimer {
 };
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+inline bool aligned4(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 3u) == 0; }
 
 // True when every row that starts at `base + i * strides[j]` (element strides,
 // fp16 elements) is 16-byte aligned.

@@ -71,6 +71,8 @@ struct PrefillParams {
   const half_t* v;
   half_t* o;
   const void* varlen;
+  float* lse;  // optional [B, Hq, S] natural-log normaliser
+  int64_t lse_sb, lse_sh, lse_ss;
   int64_t q_sb, q_sh, q_ss;
   int64_t k_sb, k_sh, k_ss;
   int64_t v_sb, v_sh, v_ss;
@@ -433,6 +435,13 @@ void prefill_kernel(PrefillParams p) {
     if (row >= row_lim) continue;
     const float l_row = xor32_sum(l_part[rb]);
     const float inv = l_row > 0.f ? 1.0f / l_row : 0.f;
+    if (p.lse && g == 0) {
+      // ln sum_k exp(scale * q.k) = (m + log2 l) * ln 2: P = exp2(c s - m) and
+      // l sums the fp16-rounded P (the reference's commented-out store at
+      // prefill_flash_attention.py:331-333 is m + log l in natural units).
+      p.lse[(int64_t)b * p.lse_sb + (int64_t)h * p.lse_sh + (int64_t)row * p.lse_ss] =
+          l_row > 0.f ? (m_run[rb] + __log2f(l_row)) * kLn2 : AKT_P_NEG_INF;
+    }
     half_t* orow = Oh + (int64_t)row * p.o_ss;
 #pragma unroll
     for (int n = 0; n < NT; ++n)
@@ -464,12 +473,12 @@ int launch_d(bool causal, bool varlen, const PrefillParams& p, unsigned grid, hi
 
 using namespace akt;
 
-extern "C" int akt_prefill_fwd(const void* q, const void* k, const void* v, void* o, int64_t batch,
-                               int64_t num_q_heads, int64_t num_kv_heads, int64_t seq_len,
-                               int64_t head_dim, const int64_t q_stride[4],
-                               const int64_t k_stride[4], const int64_t v_stride[4],
-                               const int64_t o_stride[4], float softmax_scale, int causal,
-                               const void* varlen, int varlen_bits, void* stream) {
+namespace {
+int prefill_impl(const void* q, const void* k, const void* v, void* o, float* lse, int64_t batch,
+                 int64_t num_q_heads, int64_t num_kv_heads, int64_t seq_len, int64_t head_dim,
+                 const int64_t q_stride[4], const int64_t k_stride[4], const int64_t v_stride[4],
+                 const int64_t o_stride[4], const int64_t* lse_stride, float softmax_scale,
+                 int causal, const void* varlen, int varlen_bits, void* stream) {
   clear_error();
   AKT_CHECK(batch >= 0 && num_q_heads > 0 && num_kv_heads > 0, "batch/head counts must be positive");
   AKT_CHECK(num_q_heads % num_kv_heads == 0,
@@ -486,6 +495,7 @@ extern "C" int akt_prefill_fwd(const void* q, const void* k, const void* v, void
             "tensors must have 16-byte aligned rows");
   AKT_CHECK(!varlen || varlen_bits == 32 || varlen_bits == 64, "varlen_bits must be 32 or 64");
   AKT_CHECK(softmax_scale > 0.f, "softmax_scale must be positive");
+  AKT_CHECK(!lse || (lse_stride && aligned4(lse)), "lse needs strides and 4-byte alignment");
   if (batch == 0 || seq_len == 0) return AKT_OK;
 
   PrefillParams p = {};
@@ -495,6 +505,12 @@ extern "C" int akt_prefill_fwd(const void* q, const void* k, const void* v, void
   p.o = (half_t*)o;
   p.varlen = varlen;
   p.varlen_bits = varlen_bits;
+  p.lse = lse;
+  if (lse) {
+    p.lse_sb = lse_stride[0];
+    p.lse_sh = lse_stride[1];
+    p.lse_ss = lse_stride[2];
+  }
   p.q_sb = q_stride[0]; p.q_sh = q_stride[1]; p.q_ss = q_stride[2];
   p.k_sb = k_stride[0]; p.k_sh = k_stride[1]; p.k_ss = k_stride[2];
   p.v_sb = v_stride[0]; p.v_sh = v_stride[1]; p.v_ss = v_stride[2];
@@ -515,4 +531,32 @@ extern "C" int akt_prefill_fwd(const void* q, const void* k, const void* v, void
   hipStream_t st = (hipStream_t)stream;
   if (head_dim == 64) return launch_d<64>(is_causal, is_var, p, (unsigned)grid, st);
   return launch_d<128>(is_causal, is_var, p, (unsigned)grid, st);
+}
+}  // namespace
+
+extern "C" int akt_prefill_fwd(const void* q, const void* k, const void* v, void* o, int64_t batch,
+                               int64_t num_q_heads, int64_t num_kv_heads, int64_t seq_len,
+                               int64_t head_dim, const int64_t q_stride[4],
+                               const int64_t k_stride[4], const int64_t v_stride[4],
+                               const int64_t o_stride[4], float softmax_scale, int causal,
+                               const void* varlen, int varlen_bits, void* stream) {
+  return prefill_impl(q, k, v, o, nullptr, batch, num_q_heads, num_kv_heads, seq_len, head_dim,
+                      q_stride, k_stride, v_stride, o_stride, nullptr, softmax_scale, causal,
+                      varlen, varlen_bits, stream);
+}
+
+extern "C" int akt_prefill_fwd_lse(const void* q, const void* k, const void* v, void* o,
+                                   float* lse, int64_t batch, int64_t num_q_heads,
+                                   int64_t num_kv_heads, int64_t seq_len, int64_t head_dim,
+                                   const int64_t q_stride[4], const int64_t k_stride[4],
+                                   const int64_t v_stride[4], const int64_t o_stride[4],
+                                   const int64_t lse_stride[3], float softmax_scale, int causal,
+                                   const void* varlen, int varlen_bits, void* stream) {
+  if (!lse) {
+    clear_error();
+    return set_error(AKT_ERR_INVALID_ARGUMENT, "lse output pointer is required");
+  }
+  return prefill_impl(q, k, v, o, lse, batch, num_q_heads, num_kv_heads, seq_len, head_dim,
+                      q_stride, k_stride, v_stride, o_stride, lse_stride, softmax_scale, causal,
+                      varlen, varlen_bits, stream);
 }

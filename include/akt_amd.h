@@ -31,6 +31,7 @@
  *   magicpig_sparsetoken_decode_flash_attention_redundant_var_len_paged_with_norm.py:166
  *                                                        magicpig_sparsetoken_flash_attention_decode_paged
  *   sparsetoken_decode_flash_attention_redundant.py:283-295 (kept-index selection, harness code)
+ *   prefill_flash_attention.py:331-334 (stubbed LSE store)  akt_prefill_fwd_lse, akt_merge_states
  */
 #ifndef AKT_AMD_H
 #define AKT_AMD_H
@@ -47,6 +48,10 @@ extern "C" {
 #define AKT_ERR_UNSUPPORTED 2      /* a valid request this build has no kernel for   */
 #define AKT_ERR_WORKSPACE 3        /* workspace missing or smaller than required      */
 #define AKT_ERR_HIP 4              /* the HIP runtime reported an error at launch     */
+
+/* Element types for entry points that accept more than one. */
+#define AKT_DTYPE_F16 0
+#define AKT_DTYPE_F32 1
 
 /* Message describing the last failure on the calling thread ("" if none). */
 const char* akt_last_error(void);
@@ -74,6 +79,45 @@ int akt_prefill_fwd(const void* q, const void* k, const void* v, void* o,
                     const int64_t v_stride[4], const int64_t o_stride[4],
                     float softmax_scale, int causal,
                     const void* varlen, int varlen_bits, void* stream);
+
+/*
+ * akt_prefill_fwd plus the natural-log softmax normaliser of every computed
+ * row: lse[b, h, s] = ln sum_k exp(scale * q_s . k) over the keys row s
+ * attends (fp32, strides lse_stride[0..2] over batch, head, row).  Rows that
+ * akt_prefill_fwd leaves unwritten are left unwritten here too.  The
+ * reference computes the same quantity and leaves its store commented out
+ * (prefill_flash_attention.py:331-334); this is its public form, for
+ * chunked prefill and akt_merge_states.
+ */
+int akt_prefill_fwd_lse(const void* q, const void* k, const void* v, void* o, float* lse,
+                        int64_t batch, int64_t num_q_heads, int64_t num_kv_heads,
+                        int64_t seq_len, int64_t head_dim,
+                        const int64_t q_stride[4], const int64_t k_stride[4],
+                        const int64_t v_stride[4], const int64_t o_stride[4],
+                        const int64_t lse_stride[3], float softmax_scale, int causal,
+                        const void* varlen, int varlen_bits, void* stream);
+
+/*
+ * Merge attention states computed over disjoint key sets.  For each of
+ * `rows` (query, head) rows and n_parts parts i:
+ *   lse_out = ln sum_i exp(lse_i),  o_out = sum_i exp(lse_i - lse_out) o_i.
+ * Parts with lse_i = -inf contribute nothing; a row with no contributing
+ * part gets o_out = 0 and lse_out = -inf.  No reference counterpart: it is
+ * the combine the reference's stubbed LSE stores
+ * (prefill_flash_attention.py:331-334, decode_flash_attention_redundant.py:225-228)
+ * would feed, for chunked prefill / decode and per-GPU shards.
+ *   o_parts: [n_parts, rows, head_dim] of type o_parts_dtype (AKT_DTYPE_F16 or
+ *   AKT_DTYPE_F32), strides o_parts_stride[0..1] (head_dim stride 1);
+ *   lse_parts: fp32 [n_parts, rows], strides lse_parts_stride[0..1];
+ *   o_out: [rows, head_dim] of type o_out_dtype, row stride o_out_row_stride;
+ *   lse_out: optional fp32 [rows], stride lse_out_row_stride.
+ *   head_dim: a multiple of 8 up to 512.
+ */
+int akt_merge_states(const void* o_parts, int o_parts_dtype, const float* lse_parts,
+                     void* o_out, int o_out_dtype, float* lse_out, int64_t n_parts,
+                     int64_t rows, int64_t head_dim, const int64_t o_parts_stride[2],
+                     const int64_t lse_parts_stride[2], int64_t o_out_row_stride,
+                     int64_t lse_out_row_stride, void* stream);
 
 /*
  * Single-token GQA decode over a dense cache.  Replaces

@@ -29,15 +29,19 @@ def _cpu(t: torch.Tensor, dtype) -> torch.Tensor:
 
 
 # --------------------------------------------------------------------------- prefill
-def prefill(Q, K, V, causal, softmax_scale, GQA_group_size=1, dtype=F64, head_chunk=16):
+def prefill(Q, K, V, causal, softmax_scale, GQA_group_size=1, dtype=F64, head_chunk=16,
+            return_lse=False):
     """prefill_flash_attention.py:415-425 (reference_implementation).
 
     repeat_interleave GQA, P = Q K^T * scale, causal tril mask to -inf,
     softmax, P V.  Evaluated per (batch, head chunk) to bound memory.
-    Returns O [B, H, S, D] in ``dtype``.
+    Returns O [B, H, S, D] in ``dtype``; with return_lse also the
+    logsumexp of the masked scaled scores [B, H, S] (the reference's
+    commented-out m + log(l) store, prefill_flash_attention.py:331-334).
     """
     B, H, S, D = Q.shape
     out = torch.empty((B, H, S, D), dtype=dtype)
+    lse = torch.empty((B, H, S), dtype=dtype)
     mask = torch.tril(torch.ones((S, S), dtype=torch.bool)) if causal else None
     for b in range(B):
         for h0 in range(0, H, head_chunk):
@@ -49,9 +53,10 @@ def prefill(Q, K, V, causal, softmax_scale, GQA_group_size=1, dtype=F64, head_ch
             p = torch.matmul(q, k.transpose(-2, -1)) * softmax_scale
             if causal:
                 p.masked_fill_(~mask, float("-inf"))
+            lse[b, h0:h1] = torch.logsumexp(p, dim=-1)
             p = torch.softmax(p, dim=-1)
             out[b, h0:h1] = torch.matmul(p, v)
-    return out
+    return (out, lse) if return_lse else out
 
 
 def prefill_varlen(Q, K, V, causal, softmax_scale, GQA_group_size, varlen, dtype=F64):
@@ -262,3 +267,20 @@ def magicpig_sparsetoken_naive_paged_attention(q, paged_kv_cache, kv_page_indptr
             lse[b, h] = torch.logsumexp(sc, dim=0)
             out[b, h] = torch.matmul(torch.softmax(sc, dim=0), v)
     return out, lse
+
+
+# --------------------------------------------------------------------------- merge
+def merge_states(o, lse, dtype=F64):
+    """Log-sum-exp merge of N partial states (no reference counterpart; the
+    combine implied by the stubbed LSE stores, prefill_flash_attention.py:331-334).
+
+    o: [N, ..., D], lse: [N, ...].  Returns (sum_i w_i o_i, ln sum_i exp(lse_i))
+    with w_i = exp(lse_i - LSE); rows with every lse_i = -inf give (0, -inf).
+    """
+    o = _cpu(o, dtype)
+    lse = _cpu(lse, dtype)
+    total = torch.logsumexp(lse, dim=0)
+    w = torch.exp(lse - total.unsqueeze(0))
+    w = torch.where(torch.isfinite(total).unsqueeze(0), w, torch.zeros_like(w))
+    out = (w.unsqueeze(-1) * o).sum(dim=0)
+    return out, total

@@ -108,3 +108,22 @@ def test_python_entry_points_validate_before_launch():
         pre.flash_attention_prefill(Q, K, K, True, 0.1, 2)  # CPU tensors are not accepted
     with pytest.raises(AssertionError):
         dec.flash_attention_decode(Q[:, :, :2], K, K, 0.1, 2)
+
+
+def test_merge_states_validates_arguments():
+    lib = N.load()
+    s2 = _i64(0, 0)
+    rc = lib.akt_merge_states(None, 0, None, None, 0, None, 2, 4, 12, s2, s2, 12, 1, None)
+    assert rc == 1 and b"multiple of 8" in lib.akt_last_error()
+    rc = lib.akt_merge_states(None, 5, None, None, 0, None, 2, 4, 64, s2, s2, 64, 1, None)
+    assert rc == 1 and b"dtype" in lib.akt_last_error()
+    rc = lib.akt_merge_states(None, 0, None, None, 0, None, 2, 0, 64, s2, s2, 64, 1, None)
+    assert rc == 0  # no rows: nothing to do
+
+
+def test_prefill_lse_requires_output():
+    lib = N.load()
+    s = _i64(64 * 64, 64, 64, 1)
+    rc = lib.akt_prefill_fwd_lse(None, None, None, None, None, 1, 4, 4, 4, 64, s, s, s, s,
+                                 _i64(16, 4, 1), 0.1, 1, None, 0, None)
+    assert rc == 1 and b"lse" in lib.akt_last_error()

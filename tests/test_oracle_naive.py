@@ -308,3 +308,54 @@ def test_magicpig_fp32_and_fp64_agree_on_well_conditioned_heads():
     o32, _ = naive.magicpig_sparsetoken_naive_paged_attention(q, pool, indptr, indices, ind, nnz,
                                                                Kp, Lp, dtype=torch.float32)
     assert torch.allclose(o64, o32.to(F64), atol=1e-4)
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_prefill_lse_matches_scalar_brute_force(causal):
+    g = torch.Generator().manual_seed(11)
+    B, H, Hkv, S, D = 1, 4, 2, 6, 8
+    Q, K, V = _rand(g, B, H, S, D), _rand(g, B, Hkv, S, D), _rand(g, B, Hkv, S, D)
+    _, lse = naive.prefill(Q, K, V, causal, 0.41, H // Hkv, return_lse=True)
+    for h in range(H):
+        kvh = h // (H // Hkv)
+        for i in range(S):
+            n = i + 1 if causal else S
+            q = Q[0, h, i].double().tolist()
+            keys = K[0, kvh, :n].double().tolist()
+            vals = V[0, kvh, :n].double().tolist()
+            _, ref = _scalar_attention(q, keys, vals, 0.41)
+            assert abs(float(lse[0, h, i]) - ref) < 1e-12
+
+
+def test_prefill_lse_causal_row0_is_the_single_score():
+    g = torch.Generator().manual_seed(12)
+    Q, K, V = _rand(g, 1, 2, 5, 16), _rand(g, 1, 2, 5, 16), _rand(g, 1, 2, 5, 16)
+    _, lse = naive.prefill(Q, K, V, True, 0.25, 1, return_lse=True)
+    ref = 0.25 * (Q[0, :, 0].double() * K[0, :, 0].double()).sum(-1)
+    assert torch.allclose(lse[0, :, 0], ref, atol=1e-12, rtol=0)
+
+
+def test_merge_of_key_splits_equals_attention_over_all_keys():
+    """Attention over disjoint key sets, merged by LSE, equals attention over
+    their union -- pins merge_states through the brute-force-pinned prefill."""
+    g = torch.Generator().manual_seed(13)
+    B, H, Sq, D = 2, 3, 5, 16
+    Q = _rand(g, B, H, Sq, D)
+    K = _rand(g, B, H, 17, D)
+    V = _rand(g, B, H, 17, D)
+    full_o, full_l = naive.prefill(Q, K, V, False, 0.3, 1, return_lse=True)
+    cuts = [0, 4, 5, 13, 17]
+    parts = [naive.prefill(Q, K[:, :, a:b].contiguous(), V[:, :, a:b].contiguous(), False, 0.3, 1,
+                           return_lse=True) for a, b in zip(cuts[:-1], cuts[1:])]
+    o = torch.stack([p[0] for p in parts])
+    lse = torch.stack([p[1] for p in parts])
+    mo, ml = naive.merge_states(o, lse)
+    assert torch.allclose(mo, full_o, atol=1e-12, rtol=0)
+    assert torch.allclose(ml, full_l, atol=1e-12, rtol=0)
+    # An empty part (lse = -inf, arbitrary o) changes nothing; all-empty rows give (0, -inf).
+    o2 = torch.cat([o, torch.full_like(o[:1], 123.0)])
+    l2 = torch.cat([lse, torch.full_like(lse[:1], float("-inf"))])
+    mo2, ml2 = naive.merge_states(o2, l2)
+    assert torch.allclose(mo2, full_o, atol=1e-12, rtol=0) and torch.allclose(ml2, full_l)
+    eo, el = naive.merge_states(torch.ones(2, 3, 4), torch.full((2, 3), float("-inf")))
+    assert (eo == 0).all() and torch.isneginf(el).all()
