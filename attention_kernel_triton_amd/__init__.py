@@ -13,6 +13,7 @@ Modules mirror the reference repository's files (KiritoHugh/attention_kernel_tri
                                                 magicpig_sparsetoken_flash_attention_decode_paged
   kept_index                                    select_kept (device kept-index selection)
   merge_states                                  merge_states (LSE merge of partial results)
+  sparse_csr                                    sparse decodes over CSR kept indices (inds + ptr)
 
 All of them run hand-written HIP kernels from libakt_amd.so (built by
 ``python -m attention_kernel_triton_amd.build``) through its C ABI.
@@ -29,4 +30,5 @@ __all__ = [
     "magicpig_sparsetoken_decode_flash_attention_redundant_var_len_paged_with_norm",
     "kept_index",
     "merge_states",
+    "sparse_csr",
 ]

@@ -269,6 +269,108 @@ def sparse_decode_paged(q, paged_kv_cache, kv_page_indptr, kv_page_indices, spar
     return (o, lse) if return_lse else o
 
 
+# --------------------------------------------------------------------------- CSR kept indices
+def _csr_meta(inds, ptr, dev, rows):
+    inds = _int32("inds", inds, dev).contiguous()
+    _need_gpu("ptr", ptr)
+    if ptr.device != dev:
+        raise ValueError(f"ptr is on {ptr.device}, expected {dev}")
+    if ptr.dtype != torch.int64:
+        raise TypeError(f"ptr must be int64, got {ptr.dtype}")
+    if ptr.dim() != 1 or ptr.numel() != rows + 1:
+        raise ValueError(f"ptr must be [B*Hq + 1] = [{rows + 1}], got {tuple(ptr.shape)}")
+    if inds.dim() != 1:
+        raise ValueError("inds must be 1-D")
+    return inds, ptr.contiguous()
+
+
+def _max_nnz_hint(max_nnz, inds):
+    # Without a device read the longest row is only bounded by the total.
+    return int(max_nnz) if max_nnz is not None else int(inds.numel())
+
+
+def sparse_decode_csr(q, K, V, inds, ptr, softmax_scale: float, return_lse: bool = False,
+                      num_splits: int = 0, max_nnz=None):
+    """Sparse-token decode over dense K/V with CSR kept indices (inds, ptr)."""
+    q = _half_rows("q", q)
+    K = _half_rows("K", K)
+    V = _half_rows("V", V)
+    dev = q.device
+    _same_device(dev, K=K, V=V)
+    B, Hq, _, D = q.shape
+    Hkv, S = K.shape[1], K.shape[2]
+    inds, ptr = _csr_meta(inds, ptr, dev, B * Hq)
+    hint = _max_nnz_hint(max_nnz, inds)
+    o = torch.empty((B, Hq, 1, D), dtype=q.dtype, device=dev)
+    lse = torch.empty((B, Hq), dtype=torch.float32, device=dev) if return_lse else None
+    lib = N.load()
+    ws_n = lib.akt_sparse_decode_workspace_size(B, Hq, D, hint, num_splits)
+    ws = N.workspace(ws_n, dev)
+    rc = lib.akt_sparse_decode_csr_fwd(N.ptr(q), N.ptr(K), N.ptr(V), N.ptr(inds), N.ptr(ptr),
+                                       N.ptr(o), N.ptr(lse), B, Hq, Hkv, S, D, hint, N.strides(q),
+                                       N.strides(K), N.strides(V), float(softmax_scale),
+                                       num_splits, N.ptr(ws), ws_n, N.stream_of(q))
+    N.check(rc, "akt_sparse_decode_csr_fwd")
+    return (o, lse) if return_lse else o
+
+
+def sparse_decode_paged_csr(q, paged_kv_cache, kv_page_indptr, kv_page_indices, inds, ptr,
+                            return_lse: bool = False, num_splits: int = 0, max_nnz=None,
+                            lsh_k=None, lsh_l=None):
+    """Sparse-token paged decode (MagicPIG when lsh_k/lsh_l given) with CSR kept indices."""
+    q = _half_rows("q", q)
+    pool = _half_rows("paged_kv_cache", paged_kv_cache)
+    dev = q.device
+    _same_device(dev, paged_kv_cache=pool)
+    indptr = _int32("kv_page_indptr", kv_page_indptr, dev).contiguous()
+    indices = _int32("kv_page_indices", kv_page_indices, dev).contiguous()
+    B, Hq, D = q.shape[0], q.shape[1], q.shape[-1]
+    q4 = q if q.dim() == 4 else q.unsqueeze(2)
+    P, _, Hkv, page, Dc = pool.shape
+    if Dc != D:
+        raise ValueError(f"head_dim mismatch: q has {D}, cache has {Dc}")
+    if indptr.numel() != B + 1:
+        raise ValueError("kv_page_indptr must have B+1 entries")
+    inds, ptr = _csr_meta(inds, ptr, dev, B * Hq)
+    hint = _max_nnz_hint(max_nnz, inds)
+    lk = ll = None
+    if lsh_k is not None or lsh_l is not None:
+        for name, t in (("K", lsh_k), ("L", lsh_l)):
+            _need_gpu(name, t)
+            if t.dtype != torch.float32 or tuple(t.shape) != (B, Hq):
+                raise ValueError(f"MagicPIG {name} must be float32 [{B}, {Hq}]")
+        lk, ll = lsh_k.contiguous(), lsh_l.contiguous()
+    o = torch.empty((B, Hq, D), dtype=q.dtype, device=dev)
+    lse = torch.empty((B, Hq), dtype=torch.float32, device=dev) if return_lse else None
+    lib = N.load()
+    ws_n = lib.akt_sparse_decode_workspace_size(B, Hq, D, hint, num_splits)
+    ws = N.workspace(ws_n, dev)
+    rc = lib.akt_sparse_decode_paged_csr_fwd(N.ptr(q4), N.ptr(pool), N.ptr(indptr),
+                                             N.ptr(indices), N.ptr(inds), N.ptr(ptr), N.ptr(lk),
+                                             N.ptr(ll), N.ptr(o), N.ptr(lse), B, Hq, Hkv, D, page,
+                                             P, hint, N.strides(q4), N.strides(pool), num_splits,
+                                             N.ptr(ws), ws_n, N.stream_of(q))
+    N.check(rc, "akt_sparse_decode_paged_csr_fwd")
+    return (o, lse) if return_lse else o
+
+
+def padded_to_csr(sparse_ind, sparse_nnz, l_max: int | None = None):
+    """(-1-padded [B, Hq, L] indices, counts [B, Hq(, 1)]) -> CSR (inds int32, ptr int64).
+
+    Row u = b * Hq + h keeps sparse_ind[b, h, :nnz[b, h]] (counts clamped to
+    [0, L], as the decode kernels do).  Device tensor ops; no host sync.
+    """
+    ind = sparse_ind
+    B, Hq, L = ind.shape
+    cnt = sparse_nnz.reshape(B * Hq).to(torch.int64).clamp(0, L if l_max is None else l_max)
+    pos = torch.arange(L, device=ind.device).unsqueeze(0)
+    keep = pos < cnt.unsqueeze(1)
+    inds = ind.reshape(B * Hq, L)[keep].to(torch.int32)
+    ptr = torch.zeros(B * Hq + 1, dtype=torch.int64, device=ind.device)
+    ptr[1:] = torch.cumsum(cnt, 0)
+    return inds, ptr
+
+
 # --------------------------------------------------------------------------- kept-index
 def kept_indices(l_max: int, mask=None, uniform=None, kept_ratio: float | None = None,
                  row_len=None, ensure_nonempty: bool = True):

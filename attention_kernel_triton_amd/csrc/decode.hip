@@ -57,6 +57,7 @@ struct SplitParams {
   const int32_t* last_len;
   const int32_t* sparse_ind;
   const int32_t* sparse_nnz;
+  const int64_t* csr_ptr;  // CSR kept-index rows: row u = sparse_ind[csr_ptr[u] .. csr_ptr[u+1])
   const float* lsh_k;
   const float* lsh_l;
   half_t* o;      // [B, Hq, D] contiguous
@@ -156,6 +157,7 @@ __device__ void chunk_span(const SplitParams& p, int b, int& cs_out, int& nch_ou
 struct Item {
   int b, kvh, hq0, nh, t0, t1, pstart, np, direct;
   int64_t pidx;
+  int64_t ind_off;  // sparse: offset of the unit's kept-index row in sparse_ind
 };
 
 // Everything needed to issue the loads of one item's groups.
@@ -264,8 +266,16 @@ __global__ __launch_bounds__(kThreads) void split_kernel(SplitParams p) {
       w.hq0 = u - w.b * p.Hq;
       w.kvh = w.hq0 / p.G;
       w.nh = 1;
-      int n = p.sparse_nnz[(int64_t)w.b * p.nnz_sb + (int64_t)w.hq0 * p.nnz_sh];
-      n = min(max(n, 0), p.l_max);
+      int n;
+      if (p.csr_ptr) {  // CSR rows: any length, no padding
+        const int64_t r0 = p.csr_ptr[u], r1 = p.csr_ptr[u + 1];
+        w.ind_off = r0;
+        n = (int)min(max(r1 - r0, (int64_t)0), (int64_t)INT32_MAX);
+      } else {  // padded rows [B, Hq, l_max] with a count per row
+        w.ind_off = (int64_t)w.b * p.ind_sb + (int64_t)w.hq0 * p.ind_sh;
+        n = p.sparse_nnz[(int64_t)w.b * p.nnz_sb + (int64_t)w.hq0 * p.nnz_sh];
+        n = min(max(n, 0), p.l_max);
+      }
       // Split c covers [c*per, min(n, (c+1)*per)); per is a multiple of 64 so
       // every split starts on a 16-token group and splits never share a group.
       const int per = ((n + p.n_split - 1) / p.n_split + 63) & ~63;
@@ -311,7 +321,7 @@ __global__ __launch_bounds__(kThreads) void split_kernel(SplitParams p) {
     cx.v_dummy = qrow0 - cx.vb;
     cx.ind_row = nullptr;
     if constexpr (SPARSE)
-      cx.ind_row = p.sparse_ind + (int64_t)w.b * p.ind_sb + (int64_t)w.hq0 * p.ind_sh;
+      cx.ind_row = p.sparse_ind + w.ind_off;
     cx.t1 = w.t1;
     cx.g_begin = w.t0 >> 4;
     cx.pstart = w.pstart;
@@ -382,8 +392,9 @@ __global__ __launch_bounds__(kThreads) void split_kernel(SplitParams p) {
       const int t = cx.ind_row[min(pos_k, t1 - 1)];
       const int lp = t >= 0 ? t / p.page_size : 0;
       kval = kval && t >= 0 && lp < cx.np;
-      // np == 0 (no pages) reads the nnz entry instead of an empty page table.
-      const int* pptr = cx.np > 0 ? p.indices + cx.pstart + min(lp, cx.np - 1) : p.sparse_nnz;
+      // np == 0 (no pages) reads the unit's first kept index (always mapped)
+      // instead of an empty page table; such tokens are never used.
+      const int* pptr = cx.np > 0 ? p.indices + cx.pstart + min(lp, cx.np - 1) : cx.ind_row;
       const int page = *pptr;
       kval = kval && page >= 0 && page < p.num_pool_pages;
       ra = page;
@@ -1206,7 +1217,8 @@ extern "C" size_t akt_sparse_decode_workspace_size(int64_t batch, int64_t num_q_
 namespace {
 
 int sparse_common(SplitParams& p, const void* q, const int32_t* sparse_ind,
-                  const int32_t* sparse_nnz, void* o, float* lse, int64_t batch,
+                  const int32_t* sparse_nnz, const int64_t* csr_ptr, void* o, float* lse,
+                  int64_t batch,
                   int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim, int64_t l_max,
                   const int64_t q_stride[4], const int64_t ind_stride[2],
                   const int64_t nnz_stride[2], int64_t num_splits, void* workspace,
@@ -1223,8 +1235,12 @@ int sparse_common(SplitParams& p, const void* q, const int32_t* sparse_ind,
   if (!workspace || workspace_bytes < need)
     return set_error(AKT_ERR_WORKSPACE, "workspace of %zu bytes required", need);
   p.q = (const half_t*)q;
+  AKT_CHECK(csr_ptr || (sparse_nnz && (sparse_ind || l_max == 0) && ind_stride && nnz_stride),
+            "kept-index pointers and strides are required");
+  AKT_CHECK(!csr_ptr || sparse_ind || batch == 0, "CSR kept indices are required");
   p.sparse_ind = sparse_ind;
   p.sparse_nnz = sparse_nnz;
+  p.csr_ptr = csr_ptr;
   p.o = (half_t*)o;
   p.lse = lse;
   p.counters = (int*)workspace;
@@ -1232,10 +1248,12 @@ int sparse_common(SplitParams& p, const void* q, const int32_t* sparse_ind,
   p.part_ml = p.part_o + (ns > 1 ? (size_t)rows * ns * head_dim : 0);
   p.q_sb = q_stride[0];
   p.q_sh = q_stride[1];
-  p.ind_sb = ind_stride[0];
-  p.ind_sh = ind_stride[1];
-  p.nnz_sb = nnz_stride[0];
-  p.nnz_sh = nnz_stride[1];
+  if (!csr_ptr) {
+    p.ind_sb = ind_stride[0];
+    p.ind_sh = ind_stride[1];
+    p.nnz_sb = nnz_stride[0];
+    p.nnz_sh = nnz_stride[1];
+  }
   p.B = (int)batch; p.Hq = (int)num_q_heads; p.Hkv = (int)num_kv_heads;
   p.G = (int)(num_q_heads / num_kv_heads);
   p.l_max = (int)l_max;
@@ -1246,21 +1264,21 @@ int sparse_common(SplitParams& p, const void* q, const int32_t* sparse_ind,
 
 }  // namespace
 
-extern "C" int akt_sparse_decode_fwd(const void* q, const void* k, const void* v,
-                                     const int32_t* sparse_ind, const int32_t* sparse_nnz,
-                                     void* o, float* lse, int64_t batch, int64_t num_q_heads,
-                                     int64_t num_kv_heads, int64_t seq_len, int64_t head_dim,
-                                     int64_t l_max, const int64_t q_stride[4],
-                                     const int64_t k_stride[4], const int64_t v_stride[4],
-                                     const int64_t ind_stride[2], const int64_t nnz_stride[2],
-                                     float softmax_scale, int64_t num_splits, void* workspace,
-                                     size_t workspace_bytes, void* stream) {
+static int sparse_dense_impl(const void* q, const void* k, const void* v,
+                             const int32_t* sparse_ind, const int32_t* sparse_nnz,
+                             const int64_t* csr_ptr, void* o, float* lse, int64_t batch,
+                             int64_t num_q_heads, int64_t num_kv_heads, int64_t seq_len,
+                             int64_t head_dim, int64_t l_max, const int64_t q_stride[4],
+                             const int64_t k_stride[4], const int64_t v_stride[4],
+                             const int64_t ind_stride[2], const int64_t nnz_stride[2],
+                             float softmax_scale, int64_t num_splits, void* workspace,
+                             size_t workspace_bytes, void* stream) {
   clear_error();
   SplitParams p = {};
   int64_t ns = 0;
-  int rc = sparse_common(p, q, sparse_ind, sparse_nnz, o, lse, batch, num_q_heads, num_kv_heads,
-                         head_dim, l_max, q_stride, ind_stride, nnz_stride, num_splits,
-                         workspace, workspace_bytes, ns);
+  int rc = sparse_common(p, q, sparse_ind, sparse_nnz, csr_ptr, o, lse, batch, num_q_heads,
+                         num_kv_heads, head_dim, l_max, q_stride, ind_stride, nnz_stride,
+                         num_splits, workspace, workspace_bytes, ns);
   if (rc) return rc;
   AKT_CHECK(seq_len >= 0 && seq_len < (1ll << 31), "seq_len out of range");
   AKT_CHECK(k_stride[3] == 1 && v_stride[3] == 1, "head_dim stride must be 1");
@@ -1280,9 +1298,42 @@ extern "C" int akt_sparse_decode_fwd(const void* q, const void* k, const void* v
                                                   (hipStream_t)stream);
 }
 
+extern "C" int akt_sparse_decode_fwd(const void* q, const void* k, const void* v,
+                                     const int32_t* sparse_ind, const int32_t* sparse_nnz,
+                                     void* o, float* lse, int64_t batch, int64_t num_q_heads,
+                                     int64_t num_kv_heads, int64_t seq_len, int64_t head_dim,
+                                     int64_t l_max, const int64_t q_stride[4],
+                                     const int64_t k_stride[4], const int64_t v_stride[4],
+                                     const int64_t ind_stride[2], const int64_t nnz_stride[2],
+                                     float softmax_scale, int64_t num_splits, void* workspace,
+                                     size_t workspace_bytes, void* stream) {
+  return sparse_dense_impl(q, k, v, sparse_ind, sparse_nnz, nullptr, o, lse, batch, num_q_heads,
+                           num_kv_heads, seq_len, head_dim, l_max, q_stride, k_stride, v_stride,
+                           ind_stride, nnz_stride, softmax_scale, num_splits, workspace,
+                           workspace_bytes, stream);
+}
+
+extern "C" int akt_sparse_decode_csr_fwd(const void* q, const void* k, const void* v,
+                                         const int32_t* inds, const int64_t* ptr, void* o,
+                                         float* lse, int64_t batch, int64_t num_q_heads,
+                                         int64_t num_kv_heads, int64_t seq_len, int64_t head_dim,
+                                         int64_t max_nnz, const int64_t q_stride[4],
+                                         const int64_t k_stride[4], const int64_t v_stride[4],
+                                         float softmax_scale, int64_t num_splits,
+                                         void* workspace, size_t workspace_bytes, void* stream) {
+  if (!ptr) {
+    clear_error();
+    return set_error(AKT_ERR_INVALID_ARGUMENT, "CSR row pointer is required");
+  }
+  return sparse_dense_impl(q, k, v, inds, nullptr, ptr, o, lse, batch, num_q_heads, num_kv_heads,
+                           seq_len, head_dim, max_nnz, q_stride, k_stride, v_stride, nullptr,
+                           nullptr, softmax_scale, num_splits, workspace, workspace_bytes, stream);
+}
+
 static int sparse_paged_impl(bool magic, const void* q, const void* kv_cache,
                              const int32_t* kv_page_indptr, const int32_t* kv_page_indices,
                              const int32_t* sparse_ind, const int32_t* sparse_nnz,
+                             const int64_t* csr_ptr,
                              const float* lsh_k, const float* lsh_l, void* o, float* lse,
                              int64_t batch, int64_t num_q_heads, int64_t num_kv_heads,
                              int64_t head_dim, int64_t page_size, int64_t num_pool_pages,
@@ -1293,9 +1344,9 @@ static int sparse_paged_impl(bool magic, const void* q, const void* kv_cache,
   clear_error();
   SplitParams p = {};
   int64_t ns = 0;
-  int rc = sparse_common(p, q, sparse_ind, sparse_nnz, o, lse, batch, num_q_heads, num_kv_heads,
-                         head_dim, l_max, q_stride, ind_stride, nnz_stride, num_splits,
-                         workspace, workspace_bytes, ns);
+  int rc = sparse_common(p, q, sparse_ind, sparse_nnz, csr_ptr, o, lse, batch, num_q_heads,
+                         num_kv_heads, head_dim, l_max, q_stride, ind_stride, nnz_stride,
+                         num_splits, workspace, workspace_bytes, ns);
   if (rc) return rc;
   AKT_CHECK(page_size > 0 && page_size < (1 << 20), "page_size out of range");
   AKT_CHECK(num_pool_pages >= 0, "num_pool_pages out of range");
@@ -1332,7 +1383,7 @@ extern "C" int akt_sparse_decode_paged_fwd(
     float softmax_scale, int64_t num_splits, void* workspace, size_t workspace_bytes,
     void* stream) {
   return sparse_paged_impl(false, q, kv_cache, kv_page_indptr, kv_page_indices, sparse_ind,
-                           sparse_nnz, nullptr, nullptr, o, lse, batch, num_q_heads, num_kv_heads,
+                           sparse_nnz, nullptr, nullptr, nullptr, o, lse, batch, num_q_heads, num_kv_heads,
                            head_dim, page_size, num_pool_pages, l_max, q_stride, kv_stride,
                            ind_stride, nnz_stride, softmax_scale, num_splits, workspace,
                            workspace_bytes, stream);
@@ -1347,8 +1398,27 @@ extern "C" int akt_magicpig_decode_paged_fwd(
     const int64_t ind_stride[2], const int64_t nnz_stride[2], int64_t num_splits, void* workspace,
     size_t workspace_bytes, void* stream) {
   return sparse_paged_impl(true, q, kv_cache, kv_page_indptr, kv_page_indices, sparse_ind,
-                           sparse_nnz, lsh_k, lsh_l, o, lse, batch, num_q_heads, num_kv_heads,
-                           head_dim, page_size, num_pool_pages, l_max, q_stride, kv_stride,
-                           ind_stride, nnz_stride, 1.0f / sqrtf((float)head_dim), num_splits,
-                           workspace, workspace_bytes, stream);
+                           sparse_nnz, nullptr, lsh_k, lsh_l, o, lse, batch, num_q_heads,
+                           num_kv_heads, head_dim, page_size, num_pool_pages, l_max, q_stride,
+                           kv_stride, ind_stride, nnz_stride, 1.0f / sqrtf((float)head_dim),
+                           num_splits, workspace, workspace_bytes, stream);
+}
+
+extern "C" int akt_sparse_decode_paged_csr_fwd(
+    const void* q, const void* kv_cache, const int32_t* kv_page_indptr,
+    const int32_t* kv_page_indices, const int32_t* inds, const int64_t* ptr, const float* lsh_k,
+    const float* lsh_l, void* o, float* lse, int64_t batch, int64_t num_q_heads,
+    int64_t num_kv_heads, int64_t head_dim, int64_t page_size, int64_t num_pool_pages,
+    int64_t max_nnz, const int64_t q_stride[4], const int64_t kv_stride[5], int64_t num_splits,
+    void* workspace, size_t workspace_bytes, void* stream) {
+  if (!ptr) {
+    clear_error();
+    return set_error(AKT_ERR_INVALID_ARGUMENT, "CSR row pointer is required");
+  }
+  const bool magic = lsh_k || lsh_l;
+  return sparse_paged_impl(magic, q, kv_cache, kv_page_indptr, kv_page_indices, inds, nullptr, ptr,
+                           lsh_k, lsh_l, o, lse, batch, num_q_heads, num_kv_heads, head_dim,
+                           page_size, num_pool_pages, max_nnz, q_stride, kv_stride, nullptr,
+                           nullptr, 1.0f / sqrtf((float)head_dim), num_splits, workspace,
+                           workspace_bytes, stream);
 }

@@ -32,6 +32,7 @@
  *                                                        magicpig_sparsetoken_flash_attention_decode_paged
  *   sparsetoken_decode_flash_attention_redundant.py:283-295 (kept-index selection, harness code)
  *   prefill_flash_attention.py:331-334 (stubbed LSE store)  akt_prefill_fwd_lse, akt_merge_states
+ *   sparse_decode_flash_attention.py:13-15 (CSR index note)   akt_sparse_decode_*csr_fwd
  */
 #ifndef AKT_AMD_H
 #define AKT_AMD_H
@@ -226,6 +227,41 @@ int akt_magicpig_decode_paged_fwd(const void* q, const void* kv_cache,
                                   const int64_t ind_stride[2], const int64_t nnz_stride[2],
                                   int64_t num_splits, void* workspace, size_t workspace_bytes,
                                   void* stream);
+
+/*
+ * Sparse-token decode with kept indices in CSR form (inds + ptr) instead of
+ * the -1-padded [batch, num_q_heads, l_max] rows: row u = b * num_q_heads + h
+ * keeps the tokens inds[ptr[u] .. ptr[u+1]) (int32 token positions, int64
+ * row pointer [batch * num_q_heads + 1]).  The second index format proposed
+ * in sparse_decode_flash_attention.py:13-15 (no padding, no l_max); results
+ * equal akt_sparse_decode_fwd on the same kept tokens.  max_nnz is a planning
+ * hint (the longest row) for the automatic split count and the workspace size
+ * (akt_sparse_decode_workspace_size with l_max = max_nnz); rows of any length
+ * are handled.  Other arguments as akt_sparse_decode_fwd.
+ */
+int akt_sparse_decode_csr_fwd(const void* q, const void* k, const void* v, const int32_t* inds,
+                              const int64_t* ptr, void* o, float* lse, int64_t batch,
+                              int64_t num_q_heads, int64_t num_kv_heads, int64_t seq_len,
+                              int64_t head_dim, int64_t max_nnz, const int64_t q_stride[4],
+                              const int64_t k_stride[4], const int64_t v_stride[4],
+                              float softmax_scale, int64_t num_splits, void* workspace,
+                              size_t workspace_bytes, void* stream);
+
+/*
+ * Sparse paged decode (and, with lsh_k / lsh_l given, the MagicPIG with-norm
+ * variant) with CSR kept indices; see akt_sparse_decode_csr_fwd for the CSR
+ * format and akt_sparse_decode_paged_fwd / akt_magicpig_decode_paged_fwd for
+ * the rest.  Scale 1/sqrt(head_dim).
+ */
+int akt_sparse_decode_paged_csr_fwd(const void* q, const void* kv_cache,
+                                    const int32_t* kv_page_indptr, const int32_t* kv_page_indices,
+                                    const int32_t* inds, const int64_t* ptr, const float* lsh_k,
+                                    const float* lsh_l, void* o, float* lse, int64_t batch,
+                                    int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
+                                    int64_t page_size, int64_t num_pool_pages, int64_t max_nnz,
+                                    const int64_t q_stride[4], const int64_t kv_stride[5],
+                                    int64_t num_splits, void* workspace, size_t workspace_bytes,
+                                    void* stream);
 
 /*
  * Kept-token index selection (the reference harness step at

@@ -127,3 +127,15 @@ def test_prefill_lse_requires_output():
     rc = lib.akt_prefill_fwd_lse(None, None, None, None, None, 1, 4, 4, 4, 64, s, s, s, s,
                                  _i64(16, 4, 1), 0.1, 1, None, 0, None)
     assert rc == 1 and b"lse" in lib.akt_last_error()
+
+
+def test_csr_entry_points_require_row_pointer():
+    lib = N.load()
+    s = _i64(4 * 64, 64, 64, 1)
+    rc = lib.akt_sparse_decode_csr_fwd(None, None, None, None, None, None, None, 1, 4, 4, 10, 64,
+                                       8, s, s, s, 0.1, 0, None, 0, None)
+    assert rc == 1 and b"row pointer" in lib.akt_last_error()
+    s5 = _i64(2 * 16 * 64, 16 * 64, 16 * 64, 64, 1)
+    rc = lib.akt_sparse_decode_paged_csr_fwd(None, None, None, None, None, None, None, None, None,
+                                             None, 1, 4, 4, 64, 16, 1, 8, s, s5, 0, None, 0, None)
+    assert rc == 1 and b"row pointer" in lib.akt_last_error()
