@@ -14,6 +14,7 @@ Modules mirror the reference repository's files (KiritoHugh/attention_kernel_tri
   kept_index                                    select_kept (device kept-index selection)
   merge_states                                  merge_states (LSE merge of partial results)
   sparse_csr                                    sparse decodes over CSR kept indices (inds + ptr)
+  paged_kv                                      append_paged_kv, PagedKVCache (paged KV write side)
 
 All of them run hand-written HIP kernels from libakt_amd.so (built by
 ``python -m attention_kernel_triton_amd.build``) through its C ABI.
@@ -31,4 +32,5 @@ __all__ = [
     "kept_index",
     "merge_states",
     "sparse_csr",
+    "paged_kv",
 ]

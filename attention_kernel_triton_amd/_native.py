@@ -54,6 +54,8 @@ _SIGNATURES = {
     "akt_sparse_decode_paged_csr_fwd": (C.c_int, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64,
                                                   _i64, _i64, _i64, _i64, _i64, _i64, _i64x,
                                                   _i64x, _i64, _p, C.c_size_t, _p]),
+    "akt_paged_kv_append": (C.c_int, [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64,
+                                      _i64, _i64x, _i64x, _i64x, _p]),
     "akt_kept_index_from_mask": (C.c_int, [_p, _i64, _i64, _i64, _p, _p, _i64, _p, C.c_int, _p]),
     "akt_kept_index_from_uniform": (C.c_int, [_p, C.c_float, _i64, _i64, _i64, _p, _p, _i64, _p,
                                               C.c_int, _p]),

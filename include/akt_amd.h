@@ -33,6 +33,8 @@
  *   sparsetoken_decode_flash_attention_redundant.py:283-295 (kept-index selection, harness code)
  *   prefill_flash_attention.py:331-334 (stubbed LSE store)  akt_prefill_fwd_lse, akt_merge_states
  *   sparse_decode_flash_attention.py:13-15 (CSR index note)   akt_sparse_decode_*csr_fwd
+ *   decode_flash_attention_redundant_var_len_paged.py:349-353 (page tables, harness)
+ *                                                        akt_paged_kv_append
  */
 #ifndef AKT_AMD_H
 #define AKT_AMD_H
@@ -262,6 +264,27 @@ int akt_sparse_decode_paged_csr_fwd(const void* q, const void* kv_cache,
                                     const int64_t q_stride[4], const int64_t kv_stride[5],
                                     int64_t num_splits, void* workspace, size_t workspace_bytes,
                                     void* stream);
+
+/*
+ * Paged KV cache write side: append new tokens into the page pool.
+ * Sequence b's n_b = append_indptr[b+1] - append_indptr[b] new tokens
+ * (rows of k_new / v_new: [total_new, num_kv_heads, head_dim], strides
+ * *_new_stride[0..2]) become the last n_b logical positions of b under the
+ * page table kv_page_indptr / kv_page_indices / kv_last_page_len, which must
+ * already include them (see attention_kernel_triton_amd.paged_kv.PagedKVCache).
+ * Writes pool[page, 0, h, slot] (K) and pool[page, 1, h, slot] (V) with the
+ * decode kernels' addressing; tokens whose position or page id is outside
+ * the table or pool are skipped.  No reference counterpart: the reference's
+ * tests build page tables by hand
+ * (decode_flash_attention_redundant_var_len_paged.py:349-353).
+ */
+int akt_paged_kv_append(const void* k_new, const void* v_new, const int32_t* append_indptr,
+                        void* kv_cache, const int32_t* kv_page_indptr,
+                        const int32_t* kv_page_indices, const int32_t* kv_last_page_len,
+                        int64_t batch, int64_t total_new, int64_t num_kv_heads,
+                        int64_t head_dim, int64_t page_size, int64_t num_pool_pages,
+                        const int64_t k_new_stride[3], const int64_t v_new_stride[3],
+                        const int64_t kv_stride[5], void* stream);
 
 /*
  * Kept-token index selection (the reference harness step at

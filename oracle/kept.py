@@ -58,3 +58,33 @@ def paged_seq_len(indptr: np.ndarray, last_len: np.ndarray, b: int, page: int) -
     if n <= 0:
         return 0
     return (n - 1) * page + int(min(max(last_len[b], 0), page))
+
+
+def paged_append(pool: np.ndarray, k_new: np.ndarray, v_new: np.ndarray,
+                 append_indptr: np.ndarray, indptr: np.ndarray, indices: np.ndarray,
+                 last_len: np.ndarray) -> np.ndarray:
+    """Write side of the paged layout (no reference counterpart; the reference's
+    tests build page tables by hand, decode_flash_attention_redundant_var_len_paged.py:349-353).
+
+    pool: [P, 2, Hkv, page, D]; k_new / v_new: [total_new, Hkv, D].  Sequence
+    b's new rows append_indptr[b]:append_indptr[b+1] become its last logical
+    positions under the (updated) table; positions / page ids outside the
+    table or pool are skipped.  Returns the updated copy of the pool.
+    """
+    out = pool.copy()
+    P, page = pool.shape[0], pool.shape[3]
+    B = len(indptr) - 1
+    for b in range(B):
+        a0, a1 = int(append_indptr[b]), int(append_indptr[b + 1])
+        n_new = a1 - a0
+        length = paged_seq_len(indptr, last_len, b, page)
+        for j in range(n_new):
+            t = length - n_new + j
+            if t < 0 or t >= length:
+                continue
+            pid, slot = paged_token_address(indptr, indices, b, t, page)
+            pid, slot = int(pid), int(slot)
+            if 0 <= pid < P:
+                out[pid, 0, :, slot] = k_new[a0 + j]
+                out[pid, 1, :, slot] = v_new[a0 + j]
+    return out

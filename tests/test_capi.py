@@ -139,3 +139,18 @@ def test_csr_entry_points_require_row_pointer():
     rc = lib.akt_sparse_decode_paged_csr_fwd(None, None, None, None, None, None, None, None, None,
                                              None, 1, 4, 4, 64, 16, 1, 8, s, s5, 0, None, 0, None)
     assert rc == 1 and b"row pointer" in lib.akt_last_error()
+
+
+def test_paged_append_validates_arguments():
+    lib = N.load()
+    s3 = _i64(2 * 64, 64, 1)
+    s5 = _i64(2 * 2 * 16 * 64, 2 * 16 * 64, 16 * 64, 64, 1)
+    rc = lib.akt_paged_kv_append(None, None, None, None, None, None, None, 1, 4, 2, 60, 16, 8, s3,
+                                 s3, s5, None)
+    assert rc == 1 and b"multiple of 8" in lib.akt_last_error()
+    rc = lib.akt_paged_kv_append(None, None, None, None, None, None, None, 1, 4, 2, 64, 16, 8, s3,
+                                 s3, s5, None)
+    assert rc == 1 and b"pointers" in lib.akt_last_error()
+    rc = lib.akt_paged_kv_append(None, None, None, None, None, None, None, 1, 0, 2, 64, 16, 8, s3,
+                                 s3, s5, None)
+    assert rc == 0  # nothing to append
