@@ -150,6 +150,37 @@ __device__ void chunk_span(const SplitParams& p, int b, int& cs_out, int& nch_ou
   nch_out = mine;
 }
 
+// MagicPIG correction ln u for one token (eq. 11 of the reference's
+// attention_with_norm.png, as evaluated in
+// magicpig_sparsetoken_decode_flash_attention_redundant_var_len_paged_with_norm.py:110-160):
+//   p = 1 - acos(c) / pi (clamped to [0, 1]),  x = p^K,
+//   u = 1 - (1 - x)^L - L x (1 - x)^(L - 1),  clamped to >= 1e-10.
+// u is a difference of nearly equal terms when x is small or L is near 1, so
+// it is evaluated in fp32 in a form without that cancellation:
+//   u = 1 - (1 - x)^(L - 1) (1 + (L - 1) x)
+//     = -expm1((L - 1) log1p(-x) + log1p((L - 1) x))          (x >= 0.05)
+//   u = sum_{k >= 2} (k - 1) C(L, k) (-x)^k,  k <= 8            (x < 0.05)
+// (series truncation < 1e-9 relative; both forms agree with the fp64 formula).
+__device__ __forceinline__ float magicpig_log_u(float cosv, float K, float L) {
+  const float pp = fminf(fmaxf(1.0f - acosf(cosv) * (float)M_1_PI, 0.0f), 1.0f);
+  const float x = pp > 0.0f ? __expf(K * __logf(pp)) : 0.0f;
+  float u;
+  if (x >= 0.05f) {
+    u = -expm1f((L - 1.0f) * log1pf(-x) + log1pf((L - 1.0f) * x));
+  } else {
+    float c = 0.5f * L * (L - 1.0f);  // C(L, 2)
+    float xp = x * x;
+    u = c * xp;
+#pragma unroll
+    for (int k = 3; k <= 8; ++k) {
+      c *= (L - (float)(k - 1)) / (float)k;
+      xp *= -x;
+      u = __builtin_fmaf((float)(k - 1) * c, xp, u);
+    }
+  }
+  return __logf(fmaxf(u, 1e-10f));
+}
+
 // ---------------------------------------------------------------------------
 // Split kernel.
 // ---------------------------------------------------------------------------
@@ -488,14 +519,7 @@ __global__ __launch_bounds__(kThreads) void split_kernel(SplitParams p) {
         const float dotp = sacc[r];
         float cosv = dotp / (q_norm * kn + 1e-8f);
         cosv = fminf(fmaxf(cosv, -1.0f + 1e-7f), 1.0f - 1e-7f);
-        double pi = 1.0 - (1.0 / M_PI) * acos((double)cosv);
-        pi = fmin(fmax(pi, 0.0), 1.0);
-        const double xk = pow(pi, (double)lsh_k);
-        double om = fmin(fmax(1.0 - xk, 0.0), 1.0);
-        const double L = (double)lsh_l;
-        double u = 1.0 - pow(om, L) - L * xk * pow(om, L - 1.0);
-        u = fmax(u, 1e-10);
-        const float sc = dotp * p.inv_sqrt_d - (float)log(u);
+        const float sc = dotp * p.inv_sqrt_d - magicpig_log_u(cosv, lsh_k, lsh_l);
         t[r] = ((vmask >> tt) & 1) ? sc * kLog2e : AKT_NEG_INF;
       }
     } else {
@@ -1010,11 +1034,13 @@ int launch_d(int D, int gt, const SplitParams& p, dim3 grid, dim3 cgrid, hipStre
 
 // Automatic chunk length for dense / paged caches: the smallest supported
 // length (128, 256, 512) that keeps the item count near 4096.
-// Smallest supported chunk that cuts the launch into at most ~2048 items:
-// enough to balance a persistent grid of a few hundred workgroups, few enough
-// that the combine reads a handful of partials per unit.
+// Smallest supported chunk that cuts the launch into at most ~256 items
+// (in practice the largest chunk unless the launch is tiny): an item carries a
+// fixed cost (startup latency, the workgroup merge, a partial) that small
+// chunks do not amortise -- measured on MI355X, 512-token chunks beat 128 and
+// 256 both for config 3 (paged, ~1900 items) and config 2 (dense, 256 items).
 int64_t auto_chunk(int64_t total_tokens, int64_t units) {
-  const int64_t want = ceil_div(total_tokens * units, 2048);
+  const int64_t want = ceil_div(total_tokens * units, 256);
   int64_t c = 128;
   while (c < want && c < kMaxChunk) c <<= 1;
   return c;

@@ -58,7 +58,8 @@ def _parse():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true",
                     help="skip the CPU baseline legs (for profiler runs)")
-    ap.add_argument("--only", choices=["all", "paged", "prefill"], default="all")
+    ap.add_argument("--only", choices=["all", "paged", "prefill", "legs"], default="all",
+                    help="all = paged (headline) + prefill + the other rows' legs")
     ap.add_argument("--chunk", type=int, default=0, help="split-KV chunk tokens (0 = auto)")
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
                     help="also run one device-to-device copy of this many MiB "
@@ -190,6 +191,167 @@ def bench_prefill(args):
     return out
 
 
+# --------------------------------------------------------------------------- other rows
+# Secondary legs: one per remaining hot-path row, each with the roofline of its
+# dominant kernel.  Inputs are rotated over several copies (or kept-index sets)
+# whose total exceeds the 256 MB Infinity Cache, so HBM-bound legs are not
+# measured out of the cache.
+MALL_BYTES = 256 << 20
+
+
+def _copies(nbytes_one, floor=2):
+    return max(floor, -(-2 * MALL_BYTES // max(1, nbytes_one)))
+
+
+def _leg(name, fn_list, work, unit, bound, kernel, args, note=""):
+    """Time a leg that cycles through fn_list; work = algorithmic bytes or FLOPs per step."""
+    i = [0]
+
+    def step():
+        fn_list[i[0] % len(fn_list)]()
+        i[0] += 1
+
+    steps = max(args.steps, len(fn_list))
+    t_step, t_kern = _time_steps(step, steps, max(args.warmup, len(fn_list)))
+    scale = 1e9 if unit == "GB/s" else 1e12
+    peak = HBM_PEAK_GBS if bound == "hbm" else FP16_PEAK_TFLOPS
+    out = {"value": work / t_step / scale, "unit": unit, "ms_per_step": t_step * 1e3,
+           "work_per_step": work,
+           "roofline": {"bound": bound, "achieved": work / t_kern / scale, "peak": peak,
+                        "unit": unit, "frac": work / t_kern / scale / peak, "traffic": None,
+                        "kernel": kernel, "kernel_us": t_kern * 1e6}}
+    if note:
+        out["note"] = note
+    _log(f"{name}: {out['value']:.1f} {unit} (kernel {t_kern * 1e6:.1f} us, "
+         f"frac {out['roofline']['frac']:.3f})")
+    return out
+
+
+def _sparse_bytes(ind, nnz, group, D, qo_rows):
+    """Unique K/V rows per (batch, kv head) x 4D bytes + indices + q/o/lse."""
+    import torch
+    B, H, _ = ind.shape
+    rows = 0
+    for b in range(B):
+        for g0 in range(0, H, group):
+            sets = [ind[b, h, : int(nnz[b, h, 0])] for h in range(g0, g0 + group)]
+            rows += int(torch.unique(torch.cat(sets)).numel())
+    return rows * D * 2 * 2 + 4 * int(nnz.sum()) + qo_rows * (2 * D * 2 + 4)
+
+
+def bench_legs(args):
+    import torch
+    from attention_kernel_triton_amd import _ops, kept_index
+    from attention_kernel_triton_amd import synthetic as syn
+    from attention_kernel_triton_amd.paged_kv import append_paged_kv
+    from oracle.kept import kept_from_uniform
+    dev = torch.device("cuda:0")
+    legs = {}
+
+    _log("leg: var-len causal prefill, config 1")
+    c1 = syn.prefill_config(1)
+    d1 = c1.to(dev)
+    legs["prefill_varlen_config1"] = _leg(
+        "config 1", [lambda: _ops.prefill(d1.Q, d1.K, d1.V, True, d1.scale, varlen=d1.varlen)],
+        c1.flops(), "TFLOP/s", "mfma", "prefill_kernel<64,causal,varlen>", args,
+        "FLOPs over each sequence's valid causal pairs")
+    del d1
+    torch.cuda.empty_cache()
+
+    _log("leg: dense GQA decode, config 2")
+    c2 = syn.decode_config()
+    n2 = _copies(c2.bytes())
+    d2 = [c2.to(dev) for _ in range(n2)]
+    legs["decode_config2"] = _leg(
+        "config 2", [lambda d=d: _ops.decode(d.q, d.K, d.V, d.scale) for d in d2], c2.bytes(),
+        "GB/s", "hbm", "split_kernel<64,4,kModeDense>", args,
+        f"inputs rotated over {n2} copies")
+    del d2
+    torch.cuda.empty_cache()
+
+    _log("leg: sparse-token decode, config 4a")
+    s4 = syn.sparse_config()
+    B, H, N = s4.uniform.shape
+    ind, nnz = kept_from_uniform(s4.uniform.reshape(B * H, N).numpy(), s4.kept_ratio, s4.l_max,
+                                 s4.row_len.reshape(-1).numpy())
+    ind = torch.from_numpy(ind).reshape(B, H, -1)
+    nnz = torch.from_numpy(nnz).reshape(B, H, 1)
+    b4 = _sparse_bytes(ind, nnz, s4.group, 128, B * H)
+    n4 = _copies(s4.K.numel() * 4)
+    kv4 = [(s4.K.to(dev), s4.V.to(dev)) for _ in range(n4)]
+    q4, i4, z4 = s4.q.to(dev), ind.to(dev), nnz.to(dev)
+    legs["sparse_config4a"] = _leg(
+        "config 4a", [lambda kv=kv: _ops.sparse_decode(q4, kv[0], kv[1], i4, z4, s4.scale,
+                                                      return_lse=True) for kv in kv4],
+        b4, "GB/s", "hbm", "split_kernel<128,1,kModeSparseDense>", args,
+        f"O + LSE; K/V rotated over {n4} copies; bytes = unique kept rows per kv head")
+    del kv4
+    torch.cuda.empty_cache()
+
+    _log("leg: sparse paged + MagicPIG decode, config 4b")
+    s5 = syn.sparse_paged_config()
+    p5 = s5.paged.to(dev)
+    B, H, N = s5.uniform.shape
+    sets = []
+    nsets = 0
+    b5 = 0
+    gen = torch.Generator(device=dev).manual_seed(7)
+    while True:  # distinct kept-index sets until their gathered rows exceed 2x the cache
+        u = torch.rand((B, H, N), generator=gen, device=dev)
+        ind5, nnz5 = kept_index.select_kept(s5.l_max, uniform=u, kept_ratio=s5.kept_ratio,
+                                            row_len=s5.row_len.to(dev))
+        sets.append((ind5, nnz5))
+        nsets += 1
+        if nsets == 1:
+            b5 = _sparse_bytes(ind5.cpu(), nnz5.cpu(), s5.group, 256, B * H) + \
+                4 * (p5.indices.numel() + p5.indptr.numel())
+        if nsets * b5 >= 2 * MALL_BYTES or nsets >= 64:
+            break
+    legs["sparse_paged_config4b"] = _leg(
+        "config 4b", [lambda st=st: _ops.sparse_decode_paged(p5.q, p5.pool, p5.indptr, p5.indices,
+                                                             st[0], st[1], return_lse=True)
+                      for st in sets],
+        b5, "GB/s", "hbm", "split_kernel<256,1,kModeSparsePaged>", args,
+        f"O + LSE; {nsets} kept-index sets rotated")
+    lk, ll = s5.lsh_k.to(dev), s5.lsh_l.to(dev)
+    legs["magicpig_config4b"] = _leg(
+        "config 4b MagicPIG", [lambda st=st: _ops.sparse_decode_paged(
+            p5.q, p5.pool, p5.indptr, p5.indices, st[0], st[1], return_lse=True, lsh_k=lk,
+            lsh_l=ll) for st in sets],
+        b5, "GB/s", "hbm", "split_kernel<256,1,kModeSparsePaged,magicpig>", args,
+        f"O + LSE with norm; {nsets} kept-index sets rotated")
+    del p5, sets
+    torch.cuda.empty_cache()
+
+    _log("leg: LSE merge of partial states")
+    rows, D, parts = 8 * 64 * 1024, 64, 2
+    mo = torch.randn(parts, rows, D, device=dev).half()
+    ml = torch.randn(parts, rows, device=dev)
+    mb = parts * rows * (D * 2 + 4) + rows * (D * 2 + 4)
+    legs["merge_states"] = _leg(
+        "merge", [lambda: _ops.merge_states(mo, ml)], mb, "GB/s", "hbm", "merge_kernel<f16,f16>",
+        args, f"{parts} fp16 parts of [{rows}, {D}] (config 0's rows) -> fp16")
+    del mo, ml
+    torch.cuda.empty_cache()
+
+    _log("leg: paged KV append (prefill-sized)")
+    Bq, Hkv, D, page, T = 32, 8, 128, 16, 1024
+    pages = Bq * T // page
+    pool = torch.zeros((pages, 2, Hkv, page, D), dtype=torch.float16, device=dev)
+    perm = torch.randperm(pages, generator=torch.Generator().manual_seed(3)).to(torch.int32)
+    indptr = torch.arange(0, pages + 1, T // page, dtype=torch.int32)
+    last = torch.full((Bq,), page, dtype=torch.int32)
+    ap = torch.arange(0, Bq * T + 1, T, dtype=torch.int32)
+    kn = torch.randn(Bq * T, Hkv, D, device=dev).half()
+    vn = torch.randn(Bq * T, Hkv, D, device=dev).half()
+    t_dev = [x.to(dev) for x in (ap, indptr, perm, last)]
+    legs["paged_append"] = _leg(
+        "append", [lambda: append_paged_kv(kn, vn, t_dev[0], pool, t_dev[1], t_dev[2], t_dev[3])],
+        4 * Bq * T * Hkv * D + 4 * (pages + 2 * Bq + 2), "GB/s", "hbm", "paged_append_kernel",
+        args, f"{Bq} sequences x {T} tokens into random pages")
+    return legs
+
+
 def copy_calibration(mb):
     import torch
     n = mb * (1 << 20)
@@ -239,6 +401,8 @@ def main():
         if res["value"] is None:
             res.update({"value": pf["value"], "unit": pf["unit"],
                         "ms_per_step": pf["ms_per_step"], "roofline": pf["roofline"]})
+    if args.only in ("all", "legs"):
+        res["legs"] = bench_legs(args)
     if args.copy_calibration_mb:
         copy_calibration(args.copy_calibration_mb)
     print(json.dumps(res), flush=True)

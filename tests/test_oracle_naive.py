@@ -359,3 +359,43 @@ def test_merge_of_key_splits_equals_attention_over_all_keys():
     assert torch.allclose(mo2, full_o, atol=1e-12, rtol=0) and torch.allclose(ml2, full_l)
     eo, el = naive.merge_states(torch.ones(2, 3, 4), torch.full((2, 3), float("-inf")))
     assert (eo == 0).all() and torch.isneginf(el).all()
+
+
+def test_magicpig_u_reformulation_matches_eq11():
+    """The kernels evaluate eq. 11's u = 1 - (1-x)^L - L x (1-x)^(L-1) as
+    -expm1((L-1) log1p(-x) + log1p((L-1) x)) (x >= 0.05) or as the series
+    sum_{k>=2} (k-1) C(L,k) (-x)^k (x < 0.05).  Both are checked against eq. 11
+    evaluated with 60-digit decimals (no cancellation at that precision)."""
+    from decimal import Decimal, getcontext
+    getcontext().prec = 60
+    rng = random.Random(5)
+
+    def eq11_exact(x, L):
+        x, L = Decimal(x), Decimal(L)
+        om = 1 - x
+        return float(1 - (L * om.ln()).exp() - L * x * ((L - 1) * om.ln()).exp())
+
+    def reform(x, L):
+        return -math.expm1((L - 1) * math.log1p(-x) + math.log1p((L - 1) * x))
+
+    def series(x, L):
+        c = L * (L - 1) / 2
+        xp = x * x
+        u = c * xp
+        for k in range(3, 9):
+            c *= (L - k + 1) / k
+            xp *= -x
+            u += (k - 1) * c * xp
+        return u
+
+    for _ in range(300):
+        L = rng.uniform(1.0, 6.0)
+        x = rng.uniform(0.05, 0.999)
+        ref = eq11_exact(x, L)
+        assert abs(reform(x, L) - ref) <= 1e-12 * abs(ref) + 1e-300, (x, L)
+    for _ in range(300):
+        L = rng.uniform(1.0, 6.0)
+        x = 10 ** rng.uniform(-9, math.log10(0.05))
+        ref = eq11_exact(x, L)
+        assert abs(series(x, L) - ref) <= 1e-9 * abs(ref) + 1e-300, (x, L)
+    assert series(0.01, 1.0) == 0.0 and abs(reform(0.3, 1.0)) < 1e-15  # L = 1: u = 0
