@@ -41,7 +41,11 @@ std::vector<std::pair<hipEvent_t, hipEvent_t>> g_timer_pairs;
 KernelTimer::KernelTimer() {
   std::lock_guard<std::mutex> lk(g_timer_mu);
   if (!g_timer_on) return;
-  if (hipEventCreate(&start_) != hipSuccess || hipEventCreate(&stop_) != hipSuccess) return;
+  // No system-scope fence at the event: the stamps need no cache write-back,
+  // which would otherwise be charged to the timed kernel.
+  if (hipEventCreateWithFlags(&start_, hipEventDisableSystemFence) != hipSuccess ||
+      hipEventCreateWithFlags(&stop_, hipEventDisableSystemFence) != hipSuccess)
+    return;
   armed_ = true;
 }
 

@@ -58,8 +58,10 @@ def _parse():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true",
                     help="skip the CPU baseline legs (for profiler runs)")
-    ap.add_argument("--only", choices=["all", "paged", "prefill", "legs"], default="all",
-                    help="all = paged (headline) + prefill + the other rows' legs")
+    ap.add_argument("--only", choices=["all", "headline", "paged", "prefill", "legs"],
+                    default="all",
+                    help="all = paged (headline) + prefill + the other rows' legs; "
+                         "headline = paged + prefill")
     ap.add_argument("--chunk", type=int, default=0, help="split-KV chunk tokens (0 = auto)")
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
                     help="also run one device-to-device copy of this many MiB "
@@ -384,7 +386,7 @@ def main():
            "config": {"workload": "paged var-len GQA decode, config 3", "batch": 32,
                       "num_q_heads": 32, "num_kv_heads": 8, "head_dim": 128, "page_size": 16,
                       "seq_len": "U[256, 8192]", "parallelism": "none (1 GPU)"}}
-    if args.only in ("all", "paged"):
+    if args.only in ("all", "headline", "paged"):
         pg = bench_paged(args)
         res["value"] = pg.pop("value")
         res["ms_per_step"] = pg.pop("ms_per_step")
@@ -393,7 +395,7 @@ def main():
             res["cpu_baseline"] = pg.pop("cpu_baseline")
         res["config"].update(pg)
         torch.cuda.empty_cache()
-    if args.only in ("all", "prefill"):
+    if args.only in ("all", "headline", "prefill"):
         pf = bench_prefill(args)
         pf["config"] = {"workload": "causal GQA prefill, config 0", "batch": 8,
                         "num_q_heads": 64, "num_kv_heads": 16, "seq_len": 1024, "head_dim": 64}
