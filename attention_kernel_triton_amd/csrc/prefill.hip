@@ -22,8 +22,9 @@
 // padding; 16-byte chunk c of row r sits at chunk position c ^ swz(r), which
 // keeps both the 16-byte K reads (8 consecutive rows, one chunk) and the
 // transposing V reads (4 rows x 2 chunks per 16 lanes) free of bank
-// conflicts.  Rows past the keys a tile may use are loaded from row 0 of the
-// sequence, so every staged value is finite and in bounds.
+// conflicts.  Rows past the keys a tile may use fall outside the tile's
+// buffer-resource range and read as zeros, so every staged value is finite
+// and no read leaves the tensor.
 //
 // Per 32-key step t a wave runs, with no dependence between the three parts:
 //   O^T += V^T . P(t-1)^T   A = V^T via ds_read_b64_tr_b16, B = the previous
@@ -36,17 +37,20 @@
 // so row max / sum need one v_permlane32_swap.
 //
 // Softmax.  Scores are scaled by softmax_scale * log2(e) and exponentiated with
-// v_exp_f32.  The running max is only raised when a step's max exceeds it by
-// more than kRescaleSlack (log2 units); otherwise the stale max is kept, which
-// bounds P by 2^kRescaleSlack and skips the O rescale.  A raise rescales the
-// normaliser at once and O after the step's P.V(t-1) has been accumulated.  P
+// v_exp_f32 against the running max as it stands; no per-step row max is
+// taken.  Only when a lane's partial row sum shows a probability above
+// 2^kRescaleSlack (or a NaN, as in step 0) does the wave take a rare branch
+// that computes the row max, raises the running max of the rows that exceed
+// it by more than kRescaleSlack (log2 units), rescales their normaliser and O
+// (after the step's P.V(t-1) has been accumulated) and recomputes P.  So P
+// stays below 16 * 2^kRescaleSlack and the O rescale is almost never run.  P
 // is rounded to fp16 for P.V (as the reference does at
 // prefill_flash_attention.py:94) and the normaliser sums the same rounded values.
 //
 // Masking uses a select (score = -inf), not the reference's additive -1e6
 // (prefill_flash_attention.py:76), so non-finite padding never leaks.  In
 // var-len causal mode the K/V rows at or beyond a sequence's length are never
-// staged (row 0 is loaded in their place), so padding cannot reach valid rows
+// staged (zeros are read in their place), so padding cannot reach valid rows
 // through P.V either.
 #include <math.h>
 
@@ -62,7 +66,13 @@ constexpr int kSlots = 4;   // waves per workgroup
 constexpr int kRows = 64;   // query rows per slot (two 32-row MFMA blocks)
 constexpr int kBN = 64;     // keys per staged tile
 constexpr int kNBuf = 4;    // LDS tile buffers
+// Word 3 of a raw (stride 0) gfx9 buffer resource: 32-bit data format.
+constexpr int kBufferWord3 = 0x00020000;
 constexpr float kRescaleSlack = 8.0f;
+// Largest partial row sum of one step (16 probabilities of a lane) that
+// proves no probability exceeds 2^kRescaleSlack.
+constexpr float kStepSumLimit = 16.0f * 256.0f;
+static_assert(kRescaleSlack == 8.0f, "kStepSumLimit assumes a slack of 8");
 #define AKT_P_NEG_INF (-__builtin_inff())
 
 struct PrefillParams {
@@ -189,18 +199,31 @@ void prefill_kernel(PrefillParams p) {
 
   // ---- K/V tile staging through registers: chunk i of this thread is
   // 16-byte chunk tid + 256 i of the K (then V) tile: row st_r[i], global
-  // chunk st_c[i], stored at chunk position st_c[i] ^ swz(row).
+  // chunk st_c[i], stored at chunk position st_c[i] ^ swz(row).  Tile j is
+  // read through a buffer resource based at its first row whose range ends
+  // with row min(64, key_lim - 64 j) - 1: rows past it read as zeros, and the
+  // per-lane offsets are loop invariants, so a tile costs no address VALU.
   constexpr int PER_T = kBN * CPR / kPThreads;  // chunks per thread per matrix
   uint4_t kst[PER_T], vst[PER_T];
+  int kvo[PER_T], vvo[PER_T];
+#pragma unroll
+  for (int i = 0; i < PER_T; ++i) {
+    const int q = tid + i * kPThreads;
+    const int r = q / CPR, cc = q % CPR;
+    kvo[i] = (int)(r * p.k_ss * 2) + 16 * cc;
+    vvo[i] = (int)(r * p.v_ss * 2) + 16 * cc;
+  }
   auto load_tile = [&](int j) {
+    const int rows = uniform(min(kBN, key_lim - j * kBN));  // >= 1: tiles start below key_lim
+    const int64_t row0 = (int64_t)j * kBN;
+    const auto kr = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(Kh + row0 * p.k_ss), 0, (int)((rows - 1) * p.k_ss * 2) + ROWB, kBufferWord3);
+    const auto vr = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(Vh + row0 * p.v_ss), 0, (int)((rows - 1) * p.v_ss * 2) + ROWB, kBufferWord3);
 #pragma unroll
     for (int i = 0; i < PER_T; ++i) {
-      const int q = tid + i * kPThreads;
-      const int r = q / CPR, cc = q % CPR;
-      int key = j * kBN + r;
-      if (key >= key_lim) key = 0;
-      kst[i] = ld16(Kh + (int64_t)key * p.k_ss + 8 * cc);
-      vst[i] = ld16(Vh + (int64_t)key * p.v_ss + 8 * cc);
+      kst[i] = __builtin_bit_cast(uint4_t, __builtin_amdgcn_raw_buffer_load_b128(kr, kvo[i], 0, 0));
+      vst[i] = __builtin_bit_cast(uint4_t, __builtin_amdgcn_raw_buffer_load_b128(vr, vvo[i], 0, 0));
     }
   };
   auto store_tile = [&](int j) {
@@ -324,12 +347,34 @@ void prefill_kernel(PrefillParams p) {
     load_vf(t, vf);
     pv_mfma(vf, pk);
   };
+  // Probabilities of S(t) against the running max m_run: fp16-rounded P into
+  // pk and the lane's partial row sums into l_step.
+  auto softmax = [&](const float16_t (&ss)[2], uint32_t (&pk)[2][8], float (&l_step)[2]) {
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
+      l_step[rb] = 0.f;
+#pragma unroll
+      for (int r = 0; r < 16; r += 2) {
+        const float p0 = fast_exp2(__builtin_fmaf(ss[rb][r], c, -m_run[rb]));
+        const float p1 = fast_exp2(__builtin_fmaf(ss[rb][r + 1], c, -m_run[rb]));
+        pk[rb][r >> 1] = pack_half2(p0, p1);
+        l_step[rb] = dot2(pk[rb][r >> 1], kOnes, l_step[rb]);
+      }
+    }
+  };
   // One pipeline step t < n_h: mask S(t); then, in one scheduling region,
-  // the fragment reads, the max of S(t), P.V(t-1), S(t+1) and exp of S(t) --
-  // the MFMAs and the softmax VALU work are independent, so the scheduler can
-  // interleave them and keep both pipes busy; then the rare O / normaliser
-  // rescale, applied after P.V(t-1) (computed on the old max) has been
-  // accumulated.
+  // the fragment reads, P.V(t-1), S(t+1) and the probabilities of S(t) -- the
+  // MFMAs and the softmax VALU work are independent, so the scheduler can
+  // interleave them and keep both pipes busy.  The probabilities use the
+  // running max as it stands, so no per-step row max is needed: a lane's 16
+  // probabilities of a row sum to at most 16 * 2^kRescaleSlack unless one of
+  // them exceeds 2^kRescaleSlack.  A larger (or NaN) sum -- always the case in
+  // step 0, where m_run = -inf -- takes the rare branch: the row max is
+  // computed, rows whose max exceeds m_run by more than kRescaleSlack (log2
+  // units) raise m_run, the normaliser and O are rescaled (after P.V(t-1),
+  // computed on the old max, has been accumulated) and the step's
+  // probabilities are recomputed.  Otherwise every P stays below
+  // 16 * 2^kRescaleSlack, far inside fp16's range.
   auto step = [&](int t, float16_t (&scur)[2], float16_t (&snext)[2],
                   const uint32_t (&pprev)[2][8], uint32_t (&pcur)[2][8]) {
     const int kh0 = t * 32;
@@ -346,55 +391,37 @@ void prefill_kernel(PrefillParams p) {
     load_vf(t > 0 ? t - 1 : 0, vf);
     load_kf(t + 1, kf);
 
-    // Every row has a valid key in step 0 (key 0: causal rows are >= 0 and
-    // S >= 1), so the running max is finite from step 0 on and needs no -inf
-    // guard.  IEEE maximum (NaN-propagating) needs no operand canonicalisation.
-    float m_new[2];
-    bool need_any = false;
-#pragma unroll
-    for (int rb = 0; rb < 2; ++rb) {
-      float mx = scur[rb][0];
-#pragma unroll
-      for (int r = 1; r < 16; ++r) mx = __builtin_elementwise_maximum(mx, scur[rb][r]);
-      float a, b;
-      swap32(mx, a, b);
-      mx = __builtin_elementwise_maximum(a, b) * c;
-      const bool need = mx > m_run[rb] + kRescaleSlack;
-      m_new[rb] = need ? mx : m_run[rb];
-      need_any |= need;
-    }
-    const bool rescale = __any(need_any);
-
     pv_mfma(vf, pprev);
     qk_mfma(kf, snext);
 
     float l_step[2];
+    softmax(scur, pcur, l_step);
+    bool over = false;
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb) {
-      l_step[rb] = 0.f;
-#pragma unroll
-      for (int r = 0; r < 16; r += 2) {
-        const float p0 = fast_exp2(__builtin_fmaf(scur[rb][r], c, -m_new[rb]));
-        const float p1 = fast_exp2(__builtin_fmaf(scur[rb][r + 1], c, -m_new[rb]));
-        pcur[rb][r >> 1] = pack_half2(p0, p1);
-        l_step[rb] = dot2(pcur[rb][r >> 1], kOnes, l_step[rb]);
-      }
-    }
-    // Keep the exp phase ahead of the rescale branch: without a use here the
-    // compiler sinks it past the branch, away from the MFMAs it overlaps.
-    asm volatile("" ::"v"(l_step[0]), "v"(l_step[1]));
-
-    if (rescale) {  // wave-uniform, rare
+    for (int rb = 0; rb < 2; ++rb) over |= !(l_step[rb] <= kStepSumLimit);
+    if (__any(over)) {  // wave-uniform, rare
+      // Every row has a valid key in step 0 (key 0: causal rows are >= 0 and
+      // S >= 1), so the max of a row raised here is finite.  IEEE maximum
+      // (NaN-propagating) needs no operand canonicalisation.
 #pragma unroll
       for (int rb = 0; rb < 2; ++rb) {
-        const float alpha = m_new[rb] > m_run[rb] ? fast_exp2(m_run[rb] - m_new[rb]) : 1.0f;
-        l_part[rb] *= alpha;
-        m_run[rb] = m_new[rb];
+        float mx = scur[rb][0];
 #pragma unroll
-        for (int n = 0; n < NT; ++n)
+        for (int r = 1; r < 16; ++r) mx = __builtin_elementwise_maximum(mx, scur[rb][r]);
+        float a, b;
+        swap32(mx, a, b);
+        mx = __builtin_elementwise_maximum(a, b) * c;
+        if (mx > m_run[rb] + kRescaleSlack) {
+          const float alpha = fast_exp2(m_run[rb] - mx);  // 0 while m_run = -inf
+          l_part[rb] *= alpha;
+          m_run[rb] = mx;
 #pragma unroll
-          for (int r = 0; r < 16; ++r) oacc[rb][n][r] *= alpha;
+          for (int n = 0; n < NT; ++n)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) oacc[rb][n][r] *= alpha;
+        }
       }
+      softmax(scur, pcur, l_step);
     }
 #pragma unroll
     for (int rb = 0; rb < 2; ++rb) l_part[rb] += l_step[rb];
@@ -496,6 +523,10 @@ int prefill_impl(const void* q, const void* k, const void* v, void* o, float* ls
   AKT_CHECK(!varlen || varlen_bits == 32 || varlen_bits == 64, "varlen_bits must be 32 or 64");
   AKT_CHECK(softmax_scale > 0.f, "softmax_scale must be positive");
   AKT_CHECK(!lse || (lse_stride && aligned4(lse)), "lse needs strides and 4-byte alignment");
+  // K / V tiles are read through 32-bit buffer offsets of up to 64 rows.
+  AKT_CHECK(k_stride[2] >= 0 && k_stride[2] < (1 << 22) && v_stride[2] >= 0 &&
+                v_stride[2] < (1 << 22),
+            "K / V sequence stride out of range [0, 2^22)");
   if (batch == 0 || seq_len == 0) return AKT_OK;
 
   PrefillParams p = {};

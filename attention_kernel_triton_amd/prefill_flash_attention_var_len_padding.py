@@ -6,8 +6,8 @@ int32/int64 tensor [B] of valid lengths of right-padded sequences.  As in the
 reference, query rows are processed in 64-row blocks up to
 ceil(varlen[b] / 64) * 64 and rows in later blocks are left unwritten; rows at
 or beyond varlen[b] are unspecified.  With causal=True a valid row never sees
-padding (padding K/V rows are never staged: the sequence's first row is loaded
-in their place, so non-finite padding cannot leak through P.V either); with
+padding (padding K/V rows are never staged: zeros are read in their place, so
+non-finite padding cannot leak through P.V either); with
 causal=False every row attends all S keys, padding included, exactly like
 the reference.
 ``varlen=None`` means every sequence has length S.
