@@ -213,7 +213,7 @@ void prefill_kernel(PrefillParams p) {
     kvo[i] = (int)(r * p.k_ss * 2) + 16 * cc;
     vvo[i] = (int)(r * p.v_ss * 2) + 16 * cc;
   }
-  auto load_tile = [&](int j) {
+  auto load_tile_to = [&](int j, uint4_t (&kd)[PER_T], uint4_t (&vd)[PER_T]) {
     const int rows = uniform(min(kBN, key_lim - j * kBN));  // >= 1: tiles start below key_lim
     const int64_t row0 = (int64_t)j * kBN;
     const auto kr = __builtin_amdgcn_make_buffer_rsrc(
@@ -222,21 +222,23 @@ void prefill_kernel(PrefillParams p) {
         (void*)(Vh + row0 * p.v_ss), 0, (int)((rows - 1) * p.v_ss * 2) + ROWB, kBufferWord3);
 #pragma unroll
     for (int i = 0; i < PER_T; ++i) {
-      kst[i] = __builtin_bit_cast(uint4_t, __builtin_amdgcn_raw_buffer_load_b128(kr, kvo[i], 0, 0));
-      vst[i] = __builtin_bit_cast(uint4_t, __builtin_amdgcn_raw_buffer_load_b128(vr, vvo[i], 0, 0));
+      kd[i] = __builtin_bit_cast(uint4_t, __builtin_amdgcn_raw_buffer_load_b128(kr, kvo[i], 0, 0));
+      vd[i] = __builtin_bit_cast(uint4_t, __builtin_amdgcn_raw_buffer_load_b128(vr, vvo[i], 0, 0));
     }
   };
-  auto store_tile = [&](int j) {
+  auto load_tile = [&](int j) { load_tile_to(j, kst, vst); };
+  auto store_tile_from = [&](int j, const uint4_t (&kd)[PER_T], const uint4_t (&vd)[PER_T]) {
     char* buf = lds + (j % kNBuf) * BUFB;
 #pragma unroll
     for (int i = 0; i < PER_T; ++i) {
       const int q = tid + i * kPThreads;
       const int r = q / CPR, cc = q % CPR;
       const int off = r * ROWB + ((cc ^ swz(r)) * 16);
-      *reinterpret_cast<uint4_t*>(buf + off) = kst[i];
-      *reinterpret_cast<uint4_t*>(buf + TILEB + off) = vst[i];
+      *reinterpret_cast<uint4_t*>(buf + off) = kd[i];
+      *reinterpret_cast<uint4_t*>(buf + TILEB + off) = vd[i];
     }
   };
+  auto store_tile = [&](int j) { store_tile_from(j, kst, vst); };
 
   // ---- per-lane LDS byte offsets (within a tile buffer) of the fragments
   // K rows for S^T: key l32 of the step, chunks g * HALF / 8 + s.
@@ -427,13 +429,16 @@ void prefill_kernel(PrefillParams p) {
     for (int rb = 0; rb < 2; ++rb) l_part[rb] += l_step[rb];
   };
 
-  load_tile(0);
-  store_tile(0);
-  if (n_tiles > 1) {
-    load_tile(1);
-    store_tile(1);
+  // Tiles 0..2 and Q are requested together (one round trip); tiles 0 and 1
+  // go to LDS, tile 2 waits in the staging registers.
+  {
+    uint4_t k0[PER_T], v0[PER_T], k1[PER_T], v1[PER_T];
+    load_tile_to(0, k0, v0);
+    if (n_tiles > 1) load_tile_to(1, k1, v1);
+    if (n_tiles > 2) load_tile(2);
+    store_tile_from(0, k0, v0);
+    if (n_tiles > 1) store_tile_from(1, k1, v1);
   }
-  if (n_tiles > 2) load_tile(2);
   __syncthreads();
   if (n_h > 0) qk(0, sA);
   // Steps run in pairs (2j, 2j + 1), one pair per tile; n_h is even.  At the
