@@ -38,14 +38,18 @@
 //
 // Softmax.  Scores are scaled by softmax_scale * log2(e) and exponentiated with
 // v_exp_f32 against the running max as it stands; no per-step row max is
-// taken.  Only when a lane's partial row sum shows a probability above
+// taken.  Only when a row's sum over the step shows a probability above
 // 2^kRescaleSlack (or a NaN, as in step 0) does the wave take a rare branch
 // that computes the row max, raises the running max of the rows that exceed
 // it by more than kRescaleSlack (log2 units), rescales their normaliser and O
 // (after the step's P.V(t-1) has been accumulated) and recomputes P.  So P
-// stays below 16 * 2^kRescaleSlack and the O rescale is almost never run.  P
+// stays below 32 * 2^kRescaleSlack and the O rescale is almost never run.  P
 // is rounded to fp16 for P.V (as the reference does at
-// prefill_flash_attention.py:94) and the normaliser sums the same rounded values.
+// prefill_flash_attention.py:94) and the normaliser sums the same rounded
+// values, on the matrix pipe (see softmax below).  That sum pairs row n with
+// row n + 16 through zero weights, so a query row holding NaN also turns its
+// partner row's output to NaN; finite inputs are unaffected, and var-len
+// padding rows are read as zeros.
 //
 // Masking uses a select (score = -inf), not the reference's additive -1e6
 // (prefill_flash_attention.py:76), so non-finite padding never leaks.  In
@@ -69,9 +73,10 @@ constexpr int kNBuf = 4;    // LDS tile buffers
 // Word 3 of a raw (stride 0) gfx9 buffer resource: 32-bit data format.
 constexpr int kBufferWord3 = 0x00020000;
 constexpr float kRescaleSlack = 8.0f;
-// Largest partial row sum of one step (16 probabilities of a lane) that
-// proves no probability exceeds 2^kRescaleSlack.
-constexpr float kStepSumLimit = 16.0f * 256.0f;
+// Largest row sum of one 32-key step that lets P stay unchecked: below it
+// every probability is under 32 * 2^kRescaleSlack, far inside fp16's range;
+// above it some probability exceeds 2^kRescaleSlack.
+constexpr float kStepSumLimit = 32.0f * 256.0f;
 static_assert(kRescaleSlack == 8.0f, "kStepSumLimit assumes a slack of 8");
 #define AKT_P_NEG_INF (-__builtin_inff())
 
@@ -263,7 +268,10 @@ void prefill_kernel(PrefillParams p) {
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
       uint4_t v = {0, 0, 0, 0};
-      if (active && row < S) v = ld16(Qh + (int64_t)row * p.q_ss + g * HALF + 8 * s);
+      // Var-len query rows at or past the length are read as zeros: their
+      // outputs are unspecified, and non-finite padding must not reach the
+      // row sums, whose MFMA pairs row n with row n + 16.
+      if (active && row < (VARLEN ? len : S)) v = ld16(Qh + (int64_t)row * p.q_ss + g * HALF + 8 * s);
       qf[rb][s] = as_half8(v);
     }
   }
@@ -350,33 +358,48 @@ void prefill_kernel(PrefillParams p) {
     pv_mfma(vf, pk);
   };
   // Probabilities of S(t) against the running max m_run: fp16-rounded P into
-  // pk and the lane's partial row sums into l_step.
+  // pk and the step's row sums into l_step.
+  // The row sums of P run on the matrix pipe: a v_mfma_f32_16x16x32_f16 takes
+  // a 16-key P^T fragment as its B operand unchanged (lane L then stands for
+  // row L & 15 + 16 ((L >> 4) & 1) and keys 8 (L >> 5) ..), and the 0/1 A
+  // operand ones_a picks, for output rows m < 8, the lanes of rows 0..15 and,
+  // for m >= 8, those of rows 16..31.  Summed over the step's two fragments,
+  // lane L's result is the full 32-key sum of row
+  // rho = (L & 15) + 16 (L >> 5); l_part keeps that layout.
+  const uint32_t ones_bits = ((((lane >> 4) & 1) == 0) == ((lane & 15) < 8)) ? kOnes : 0u;
+  const half8_t ones_a = as_half8(uint4_t{ones_bits, ones_bits, ones_bits, ones_bits});
+  const int rho = (lane & 15) + 16 * (lane >> 5);
   auto softmax = [&](const float16_t (&ss)[2], uint32_t (&pk)[2][8], float (&l_step)[2]) {
 #pragma unroll
     for (int rb = 0; rb < 2; ++rb) {
-      l_step[rb] = 0.f;
 #pragma unroll
       for (int r = 0; r < 16; r += 2) {
         const float p0 = fast_exp2(__builtin_fmaf(ss[rb][r], c, -m_run[rb]));
         const float p1 = fast_exp2(__builtin_fmaf(ss[rb][r + 1], c, -m_run[rb]));
         pk[rb][r >> 1] = pack_half2(p0, p1);
-        l_step[rb] = dot2(pk[rb][r >> 1], kOnes, l_step[rb]);
       }
+    }
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
+      float4_t ls = {0.f, 0.f, 0.f, 0.f};
+      ls = mfma16x16x32(ones_a, as_half8(uint4_t{pk[rb][0], pk[rb][1], pk[rb][2], pk[rb][3]}), ls);
+      ls = mfma16x16x32(ones_a, as_half8(uint4_t{pk[rb][4], pk[rb][5], pk[rb][6], pk[rb][7]}), ls);
+      l_step[rb] = ls[0];
     }
   };
   // One pipeline step t < n_h: mask S(t); then, in one scheduling region,
   // the fragment reads, P.V(t-1), S(t+1) and the probabilities of S(t) -- the
   // MFMAs and the softmax VALU work are independent, so the scheduler can
   // interleave them and keep both pipes busy.  The probabilities use the
-  // running max as it stands, so no per-step row max is needed: a lane's 16
-  // probabilities of a row sum to at most 16 * 2^kRescaleSlack unless one of
+  // running max as it stands, so no per-step row max is needed: the step's 32
+  // probabilities of a row sum to at most 32 * 2^kRescaleSlack unless one of
   // them exceeds 2^kRescaleSlack.  A larger (or NaN) sum -- always the case in
   // step 0, where m_run = -inf -- takes the rare branch: the row max is
   // computed, rows whose max exceeds m_run by more than kRescaleSlack (log2
   // units) raise m_run, the normaliser and O are rescaled (after P.V(t-1),
   // computed on the old max, has been accumulated) and the step's
   // probabilities are recomputed.  Otherwise every P stays below
-  // 16 * 2^kRescaleSlack, far inside fp16's range.
+  // 32 * 2^kRescaleSlack, far inside fp16's range.
   auto step = [&](int t, float16_t (&scur)[2], float16_t (&snext)[2],
                   const uint32_t (&pprev)[2][8], uint32_t (&pcur)[2][8]) {
     const int kh0 = t * 32;
@@ -413,9 +436,10 @@ void prefill_kernel(PrefillParams p) {
         float a, b;
         swap32(mx, a, b);
         mx = __builtin_elementwise_maximum(a, b) * c;
-        if (mx > m_run[rb] + kRescaleSlack) {
-          const float alpha = fast_exp2(m_run[rb] - mx);  // 0 while m_run = -inf
-          l_part[rb] *= alpha;
+        const bool raise = mx > m_run[rb] + kRescaleSlack;
+        const float alpha = raise ? fast_exp2(m_run[rb] - mx) : 1.f;  // 0 while m_run = -inf
+        l_part[rb] *= __shfl(alpha, rho, 64);  // row rho's factor (lane rho < 32 holds it)
+        if (raise) {
           m_run[rb] = mx;
 #pragma unroll
           for (int n = 0; n < NT; ++n)
@@ -465,7 +489,8 @@ void prefill_kernel(PrefillParams p) {
   for (int rb = 0; rb < 2; ++rb) {
     const int row = r0 + 32 * rb + l32;
     if (row >= row_lim) continue;
-    const float l_row = xor32_sum(l_part[rb]);
+    // Row l32's normaliser sits in lane l32 (rows 0..15) or l32 + 16.
+    const float l_row = __shfl(l_part[rb], l32 < 16 ? l32 : l32 + 16, 64);
     const float inv = l_row > 0.f ? 1.0f / l_row : 0.f;
     if (p.lse && g == 0) {
       // ln sum_k exp(scale * q.k) = (m + log2 l) * ln 2: P = exp2(c s - m) and
