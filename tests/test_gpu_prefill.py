@@ -115,3 +115,49 @@ def test_prefill_is_deterministic(dev):
     a = pre.flash_attention_prefill(*args)
     b = pre.flash_attention_prefill(*args)
     assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("G", [2, 3, 6])
+def test_prefill_group_sizes_non_power_of_two(dev, D, G):
+    """Slots (head f % G, row block f / G) that straddle row blocks inside a workgroup."""
+    B, Hkv, S = 2, 2, 150
+    Q, K, V = _qkv(40 + G + D, B, Hkv * G, Hkv, S, D)
+    out = pre.flash_attention_prefill(Q.to(dev), K.to(dev), V.to(dev), True, 1 / math.sqrt(D), G)
+    assert_close(out, naive.prefill(Q, K, V, True, 1 / math.sqrt(D), G), what=f"G={G} D={D}")
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_prefill_rising_logits_raise_the_running_max_often(dev, causal):
+    """Scores that climb along the keys push the running max up by more than the
+    rescale slack step after step, so the rare raise-and-recompute path runs on
+    many steps, not only step 0; large magnitudes also exercise fp16 range."""
+    B, Hq, Hkv, S, D = 2, 4, 2, 384, 64
+    g = torch.Generator().manual_seed(77)
+    Q = (torch.randn(B, Hq, S, D, generator=g) * 0.2 + 1.0).half()
+    ramp = torch.linspace(0.0, 6.0, S)[None, None, :, None]
+    K = (torch.randn(B, Hkv, S, D, generator=g) * 0.2 + ramp).half()
+    V = torch.randn(B, Hkv, S, D, generator=g).half()
+    out = pre.flash_attention_prefill(Q.to(dev), K.to(dev), V.to(dev), causal, 0.125, Hq // Hkv)
+    ref = naive.prefill(Q, K, V, causal, 0.125, Hq // Hkv, dtype=torch.float32)
+    assert torch.isfinite(out.cpu()).all()
+    assert_close(out, ref, what=f"rising logits causal={causal}")
+
+
+def test_prefill_nan_query_row_leaves_rows_outside_its_pair_exact(dev):
+    """The row sums of P run on the matrix pipe and pair row n with row n + 16 of
+    the same 32-row block; every other row of a NaN query row's head is exact."""
+    B, Hq, Hkv, S, D = 1, 2, 1, 128, 64
+    Q, K, V = _qkv(91, B, Hq, Hkv, S, D)
+    bad = 37                       # row 5 of the block of rows 32..63; its pair is row 53
+    Q[0, 1, bad] = float("nan")
+    out = pre.flash_attention_prefill(Q.to(dev), K.to(dev), V.to(dev), True, 0.125, 2).cpu()
+    Qc = Q.clone()
+    Qc[0, 1, bad] = 0
+    ref = naive.prefill(Qc, K, V, True, 0.125, 2)
+    assert not torch.isfinite(out[0, 1, bad]).all()
+    keep = torch.ones(B, Hq, S, D, dtype=torch.bool)
+    keep[0, 1, bad] = False
+    keep[0, 1, (bad & ~31) + ((bad & 31) ^ 16)] = False
+    assert torch.isfinite(out[keep]).all()
+    assert_close(out, ref, what="rows outside the NaN row's pair", mask=keep)
