@@ -362,7 +362,9 @@ __global__ __launch_bounds__(kThreads) void split_kernel(SplitParams p) {
     if constexpr (MODE == kModePaged && ALIGNED) {
       const int g_end = (w.t1 + 15) >> 4;
       const int gk = cx.g_begin + wave + kWaves * lane;
-      const int gc = min(gk, g_end - 1);  // clamped: the load is issued unconditionally
+      // Clamped into the item (an empty one keeps g_begin): the load is
+      // issued unconditionally.
+      const int gc = max(min(gk, g_end - 1), cx.g_begin);
       const int lp = (gc << 4) / p.page_size;
       cx.page_pref = p.indices[w.pstart + lp];
       cx.slot_pref = (gc << 4) - lp * p.page_size;
@@ -688,6 +690,16 @@ __global__ __launch_bounds__(kThreads) void split_kernel(SplitParams p) {
     } else {
       n_items = p.B * ((p.S + p.chunk - 1) / p.chunk) * Y;
     }
+    // The item whose first groups the current item's last iterations
+    // prefetch.  Past the last item it is the current one with an empty
+    // token range: every lane then reads the unit's q row (an L2 hit) instead
+    // of re-reading K/V that left the cache long ago.
+    auto resolve_next = [&](int inext, int icur) -> Item {
+      if (inext < n_items) return resolve_persistent(inext);
+      Item w = resolve_persistent(icur);
+      w.t1 = w.t0;
+      return w;
+    };
     // Dynamic schedule: workgroup w starts with items w and w + gridDim.x,
     // then takes tickets 2 * gridDim.x, 2 * gridDim.x + 1, ... from
     // counters[0], two items ahead so the atomic's latency is hidden (and
@@ -703,7 +715,7 @@ __global__ __launch_bounds__(kThreads) void split_kernel(SplitParams p) {
     it = resolve_persistent(i);
     make_uniform(it);
     setup(it, cc, qf);
-    nx = resolve_persistent(nxt < n_items ? nxt : i);
+    nx = resolve_next(nxt, i);
     make_uniform(nx);
     setup(nx, nc, qn);
     Buf bufs[2];
@@ -724,13 +736,13 @@ __global__ __launch_bounds__(kThreads) void split_kernel(SplitParams p) {
       finish();
       const int inext = nxt;
       nxt = sm_next;
-      if (inext >= n_items) break;  // the last prefetch re-read this item (L2 hits)
+      if (inext >= n_items) break;  // the last prefetch read q rows (see resolve_next)
       i = inext;
       it = nx;
       cc = nc;
 #pragma unroll
       for (int s = 0; s < KS; ++s) qf[s] = qn[s];
-      nx = resolve_persistent(nxt < n_items ? nxt : i);
+      nx = resolve_next(nxt, i);
       make_uniform(nx);
       setup(nx, nc, qn);
     }

@@ -99,6 +99,24 @@ def _time_steps(fn, steps, warmup):
     return wall / steps, kt.total_ms / 1e3 / steps
 
 
+def _cpu_threads():
+    """The host threads the CPU baseline uses: the OMP_NUM_THREADS share when the
+    environment sets one (the GPU boxes do), else every core."""
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    return int(env) if env.isdigit() and int(env) > 0 else (os.cpu_count() or 1)
+
+
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown CPU"
+
+
 def _cpu_time(fn, reps):
     fn()  # warm-up
     ts = []
@@ -140,14 +158,15 @@ def bench_paged(args):
     if not args.no_cpu_baseline:
         from oracle import naive
         _log("CPU baseline: oracle naive_paged_attention (fp32) on config 3")
-        torch.set_num_threads(os.cpu_count() or 1)
+        torch.set_num_threads(_cpu_threads())
         reps = 3
         t = _cpu_time(lambda: naive.naive_paged_attention(
             cfg.q, cfg.pool, cfg.indptr, cfg.indices, cfg.last_len, dtype=torch.float32), reps)
         out["cpu_baseline"] = {"value": nbytes / t / 1e9, "unit": "GB/s",
                                "cores": torch.get_num_threads(), "kind": "port",
                                "sample": f"full config 3 batch, median of {reps} runs "
-                                         f"({t * 1e3:.0f} ms each), fp32 torch on CPU"}
+                                         f"({t * 1e3:.0f} ms each), fp32 torch on "
+                                         f"{torch.get_num_threads()} threads of {_cpu_model()}"}
     del p
     return out
 
@@ -181,7 +200,7 @@ def bench_prefill(args):
     if not args.no_cpu_baseline:
         from oracle import naive
         _log("CPU baseline: oracle prefill (fp32) on 2 of 8 batches of config 0")
-        torch.set_num_threads(os.cpu_count() or 1)
+        torch.set_num_threads(_cpu_threads())
         nb = 2
         reps = 3
         t = _cpu_time(lambda: naive.prefill(cfg.Q[:nb], cfg.K[:nb], cfg.V[:nb], True, cfg.scale,
@@ -189,7 +208,8 @@ def bench_prefill(args):
         out["cpu_baseline"] = {"value": flops * nb / 8 / t / 1e12, "unit": "TFLOP/s",
                                "cores": torch.get_num_threads(), "kind": "port",
                                "sample": f"2 of 8 batches of config 0, median of {reps} runs "
-                                         f"({t * 1e3:.0f} ms each), fp32 torch on CPU"}
+                                         f"({t * 1e3:.0f} ms each), fp32 torch on "
+                                         f"{torch.get_num_threads()} threads of {_cpu_model()}"}
     return out
 
 
@@ -349,7 +369,7 @@ def bench_legs(args):
     t_dev = [x.to(dev) for x in (ap, indptr, perm, last)]
     legs["paged_append"] = _leg(
         "append", [lambda: append_paged_kv(kn, vn, t_dev[0], pool, t_dev[1], t_dev[2], t_dev[3])],
-        4 * Bq * T * Hkv * D + 4 * (pages + 2 * Bq + 2), "GB/s", "hbm", "paged_append_kernel",
+        8 * Bq * T * Hkv * D + 4 * (pages + 2 * Bq + 2), "GB/s", "hbm", "paged_append_kernel",
         args, f"{Bq} sequences x {T} tokens into random pages")
     return legs
 
