@@ -38,11 +38,12 @@
 //
 // Softmax.  Scores are scaled by softmax_scale * log2(e) and exponentiated with
 // v_exp_f32 against the running max as it stands; no per-step row max is
-// taken.  Only when a row's sum over the step shows a probability above
-// 2^kRescaleSlack (or a NaN, as in step 0) does the wave take a rare branch
-// that computes the row max, raises the running max of the rows that exceed
-// it by more than kRescaleSlack (log2 units), rescales their normaliser and O
-// (after the step's P.V(t-1) has been accumulated) and recomputes P.  So P
+// taken.  The running max starts at the row max of step 0.  Only when a row's
+// sum over a step shows a probability above 2^kRescaleSlack (or a NaN) does
+// the wave take a rare branch that computes the row max, raises the running
+// max of the rows that exceed it by more than kRescaleSlack (log2 units),
+// rescales their normaliser and O (after the step's P.V(t-1) has been
+// accumulated) and recomputes P.  So P
 // stays below 32 * 2^kRescaleSlack and the O rescale is almost never run.  P
 // is rounded to fp16 for P.V (as the reference does at
 // prefill_flash_attention.py:94) and the normaliser sums the same rounded
@@ -151,6 +152,10 @@ void prefill_kernel(PrefillParams p) {
   constexpr int TILEB = kBN * ROWB;       // bytes per K (or V) tile
   constexpr int BUFB = 2 * TILEB;         // bytes per tile buffer (K then V)
   static_assert((kBN * CPR) % kPThreads == 0, "tile split");
+  // D = 64 reads the V fragments of step t + 1 at the end of step t, so P.V
+  // starts without waiting for LDS; at D = 128 they would not fit in the
+  // register budget and are read at the top of their step.
+  constexpr bool kPrefetchV = (D == 64);
 
   __shared__ __attribute__((aligned(16))) char lds[kNBuf * BUFB];
 
@@ -297,11 +302,12 @@ void prefill_kernel(PrefillParams p) {
   }
 
   float16_t sA[2], sB[2];
-  uint32_t pA[2][8], pB[2][8];
+  uint32_t pA[2][8], pB[2][8];  // pB starts as P(-1) = 0; pA is written before it is read
+  half8_t vf[2][NT];            // V fragments for the next P.V
 #pragma unroll
   for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
-    for (int i = 0; i < 8; ++i) pA[rb][i] = pB[rb][i] = 0u;
+    for (int i = 0; i < 8; ++i) pB[rb][i] = 0u;
 
   // Fragment reads of 32-key step t (its tile must be published).
   auto load_kf = [&](int t, half8_t (&kf)[KS]) {
@@ -387,14 +393,39 @@ void prefill_kernel(PrefillParams p) {
       l_step[rb] = ls[0];
     }
   };
+  // Masks S(t): keys past a row (causal) or past S read -inf.  The test is
+  // wave-uniform per 32-row block, so a causal step on the diagonal masks
+  // only the blocks that reach past it.
+  auto mask_step = [&](int t, float16_t (&ss)[2]) {
+    const int kh0 = t * 32;
+    if ((CAUSAL && kh0 + 31 > r0) || kh0 + 32 > S) {
+#pragma unroll
+      for (int rb = 0; rb < 2; ++rb) {
+        const int lim = lim_base[rb] - kh0;
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          if (8 * (r >> 2) + (r & 3) > lim) ss[rb][r] = AKT_P_NEG_INF;
+      }
+    }
+  };
+  // Row max of a masked S block in log2 units (IEEE maximum: NaN-propagating,
+  // needs no operand canonicalisation).
+  auto row_max = [&](const float16_t& sv) {
+    float mx = sv[0];
+#pragma unroll
+    for (int r = 1; r < 16; ++r) mx = __builtin_elementwise_maximum(mx, sv[r]);
+    float a, b;
+    swap32(mx, a, b);
+    return __builtin_elementwise_maximum(a, b) * c;
+  };
   // One pipeline step t < n_h: mask S(t); then, in one scheduling region,
   // the fragment reads, P.V(t-1), S(t+1) and the probabilities of S(t) -- the
   // MFMAs and the softmax VALU work are independent, so the scheduler can
   // interleave them and keep both pipes busy.  The probabilities use the
   // running max as it stands, so no per-step row max is needed: the step's 32
   // probabilities of a row sum to at most 32 * 2^kRescaleSlack unless one of
-  // them exceeds 2^kRescaleSlack.  A larger (or NaN) sum -- always the case in
-  // step 0, where m_run = -inf -- takes the rare branch: the row max is
+  // them exceeds 2^kRescaleSlack.  A larger (or NaN) sum takes the rare
+  // branch (in step 0, whose row max starts m_run, only for a NaN): the row max is
   // computed, rows whose max exceeds m_run by more than kRescaleSlack (log2
   // units) raise m_run, the normaliser and O are rescaled (after P.V(t-1),
   // computed on the old max, has been accumulated) and the step's
@@ -402,22 +433,15 @@ void prefill_kernel(PrefillParams p) {
   // 32 * 2^kRescaleSlack, far inside fp16's range.
   auto step = [&](int t, float16_t (&scur)[2], float16_t (&snext)[2],
                   const uint32_t (&pprev)[2][8], uint32_t (&pcur)[2][8]) {
-    const int kh0 = t * 32;
-    if ((CAUSAL && kh0 + 31 > r0) || kh0 + 32 > S) {  // wave-uniform
-#pragma unroll
-      for (int rb = 0; rb < 2; ++rb) {
-        const int lim = lim_base[rb] - kh0;
-#pragma unroll
-        for (int r = 0; r < 16; ++r)
-          if (8 * (r >> 2) + (r & 3) > lim) scur[rb][r] = AKT_P_NEG_INF;
-      }
-    }
-    half8_t vf[2][NT], kf[KS];
-    load_vf(t > 0 ? t - 1 : 0, vf);
+    mask_step(t, scur);  // S(0) was masked before the loop too: masking is idempotent
+    half8_t kf[KS];
+    if constexpr (!kPrefetchV) load_vf(t > 0 ? t - 1 : 0, vf);
     load_kf(t + 1, kf);
 
     pv_mfma(vf, pprev);
     qk_mfma(kf, snext);
+    // V of step t, for P.V(t) at the top of step t + 1 (its tile is published).
+    if constexpr (kPrefetchV) load_vf(t, vf);
 
     float l_step[2];
     softmax(scur, pcur, l_step);
@@ -425,19 +449,11 @@ void prefill_kernel(PrefillParams p) {
 #pragma unroll
     for (int rb = 0; rb < 2; ++rb) over |= !(l_step[rb] <= kStepSumLimit);
     if (__any(over)) {  // wave-uniform, rare
-      // Every row has a valid key in step 0 (key 0: causal rows are >= 0 and
-      // S >= 1), so the max of a row raised here is finite.  IEEE maximum
-      // (NaN-propagating) needs no operand canonicalisation.
 #pragma unroll
       for (int rb = 0; rb < 2; ++rb) {
-        float mx = scur[rb][0];
-#pragma unroll
-        for (int r = 1; r < 16; ++r) mx = __builtin_elementwise_maximum(mx, scur[rb][r]);
-        float a, b;
-        swap32(mx, a, b);
-        mx = __builtin_elementwise_maximum(a, b) * c;
+        const float mx = row_max(scur[rb]);
         const bool raise = mx > m_run[rb] + kRescaleSlack;
-        const float alpha = raise ? fast_exp2(m_run[rb] - mx) : 1.f;  // 0 while m_run = -inf
+        const float alpha = raise ? fast_exp2(m_run[rb] - mx) : 1.f;
         l_part[rb] *= __shfl(alpha, rho, 64);  // row rho's factor (lane rho < 32 holds it)
         if (raise) {
           m_run[rb] = mx;
@@ -464,11 +480,20 @@ void prefill_kernel(PrefillParams p) {
     if (n_tiles > 1) store_tile_from(1, k1, v1);
   }
   __syncthreads();
-  if (n_h > 0) qk(0, sA);
+  // S(0) (tile 0 is always staged), masked; its row max starts the running
+  // max, so step 0's probabilities are at most 1 and its sums never take the
+  // raise branch.  Every row has a valid key in step 0 (key 0: causal rows
+  // are >= 0 and S >= 1), so the start is finite for finite inputs.
+  qk(0, sA);
+  if constexpr (kPrefetchV) load_vf(0, vf);  // P.V(-1) of step 0 multiplies P = 0
+  mask_step(0, sA);
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb) m_run[rb] = row_max(sA[rb]);
   // Steps run in pairs (2j, 2j + 1), one pair per tile; n_h is even.  At the
   // top of pair j: sA = S(2j) and pB = P(2j - 1) (zero for j = 0).  The last
   // pair's S(2j + 2) is computed from whatever its buffer holds and never
   // used; the pair is followed by the drain P.V(2j + 1).
+#pragma clang loop unroll(disable)
   for (int j = 0; j < n_tiles; ++j) {
     // Publishes tile j + 1 (stored before the previous barrier) and retires
     // the buffer of tile j - 2, which now takes tile j + 2 from the staging
@@ -480,18 +505,25 @@ void prefill_kernel(PrefillParams p) {
     if (t < n_h) {  // wave-uniform
       step(t, sA, sB, pB, pA);
       step(t + 1, sB, sA, pA, pB);
-      if (t + 2 == n_h) pv(t + 1, pB);
+      if (t + 2 == n_h) {  // drain: P.V(n_h - 1)
+        if constexpr (kPrefetchV) pv_mfma(vf, pB);
+        else pv(t + 1, pB);
+      }
     }
   }
 
   if (!active) return;
+  // The row index is derived again here (the opaque copy keeps the compiler
+  // from holding the prologue's row registers live through the loop).
+  int lane_e = lane;
+  asm volatile("" : "+v"(lane_e));
 #pragma unroll
   for (int rb = 0; rb < 2; ++rb) {
-    const int row = r0 + 32 * rb + l32;
+    const int row = r0 + 32 * rb + (lane_e & 31);
     if (row >= row_lim) continue;
     // Row l32's normaliser sits in lane l32 (rows 0..15) or l32 + 16.
     const float l_row = __shfl(l_part[rb], l32 < 16 ? l32 : l32 + 16, 64);
-    const float inv = l_row > 0.f ? 1.0f / l_row : 0.f;
+    const float inv = l_row > 0.f ? __builtin_amdgcn_rcpf(l_row) : 0.f;
     if (p.lse && g == 0) {
       // ln sum_k exp(scale * q.k) = (m + log2 l) * ln 2: P = exp2(c s - m) and
       // l sums the fp16-rounded P (the reference's commented-out store at
