@@ -394,8 +394,8 @@ void prefill_kernel(PrefillParams p) {
     }
   };
   // Masks S(t): keys past a row (causal) or past S read -inf.  The test is
-  // wave-uniform per 32-row block, so a causal step on the diagonal masks
-  // only the blocks that reach past it.
+  // wave-uniform; only the steps that reach the diagonal or S run the
+  // selects.
   auto mask_step = [&](int t, float16_t (&ss)[2]) {
     const int kh0 = t * 32;
     if ((CAUSAL && kh0 + 31 > r0) || kh0 + 32 > S) {
