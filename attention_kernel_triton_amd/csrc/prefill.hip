@@ -97,7 +97,9 @@ struct PrefillParams {
   int varlen_bits;
   int n_rb;      // 64-row blocks per sequence
   int n_sg;      // slot groups (workgroups) per (batch, kv head)
-  int xcd_map;   // 1: keep a kv head's workgroups on one XCD (needs (B*Hkv) % 8 == 0)
+  int grid1d;    // 1: linear grid (a dimension past 65535); 0: grid (Hkv, B, n_sg)
+  int fast_div;  // 1: G * n_rb + kSlots < 2^22, slot / G through g_inv
+  float g_inv;   // 1 / G
   float qk_scale;  // softmax_scale * log2(e)
 };
 
@@ -118,27 +120,40 @@ __device__ __forceinline__ uint2 ds_read_tr16(const char* lds_ptr) {
 // differ in bits 1..2.
 __device__ __forceinline__ int swz(int r) { return ((r & 3) << 1) | ((r >> 2) & 1); }
 
-// Workgroup -> (batch, kv head, slot group).  Causal work is issued heaviest
-// slot group first; with xcd_map the workgroups of one kv head land on one
-// XCD (workgroup i is dispatched to XCD i % 8) so its L2 serves them all.
+// Workgroup -> (batch, kv head, slot group).  The linear workgroup id is
+// kvh + Hkv (b + B rank): causal work is issued heaviest slot group (lowest
+// rank) first, and with B * Hkv a multiple of 8 every workgroup of a kv head
+// lands on XCD (b Hkv + kvh) % 8 (workgroup i is dispatched to XCD i % 8), so
+// one L2 serves all of them.  The grid (Hkv, B, n_sg) hands out the three
+// indices without divisions; a linear grid (when a dimension exceeds 65535)
+// derives them.
 __device__ __forceinline__ void map_block(const PrefillParams& p, bool causal, int& b, int& kvh,
                                           int& sg) {
-  const int pid = blockIdx.x;
-  const int ngroups = p.B * p.Hkv;
-  int rank, kg;
-  if (p.xcd_map) {
-    const int xcd = pid & 7;
-    const int j = pid >> 3;
-    const int nk = ngroups >> 3;  // kv groups per XCD
-    rank = j / nk;
-    kg = (j - rank * nk) * 8 + xcd;
-  } else {
+  int rank;
+  if (p.grid1d) {
+    const int pid = blockIdx.x;
+    const int ngroups = p.B * p.Hkv;
     rank = pid / ngroups;
-    kg = pid - rank * ngroups;
+    const int kg = pid - rank * ngroups;
+    b = kg / p.Hkv;
+    kvh = kg - b * p.Hkv;
+  } else {
+    kvh = blockIdx.x;
+    b = blockIdx.y;
+    rank = blockIdx.z;
   }
-  b = kg / p.Hkv;
-  kvh = kg - b * p.Hkv;
   sg = causal ? (p.n_sg - 1 - rank) : rank;
+}
+
+// n / d for 0 <= n < 2^22 and d >= 1, given inv = 1 / d rounded to float:
+// the float estimate is within one of the quotient, and one correction step
+// makes it exact.  (n / d through the integer divide sequence costs several
+// dependent VALU-to-SALU round trips at the start of every workgroup.)
+__device__ __forceinline__ int div_small(int n, int d, float inv) {
+  int q = (int)((float)n * inv);
+  const int r = n - q * d;
+  q += (r >= d ? 1 : 0) - (r < 0 ? 1 : 0);
+  return q;
 }
 
 template <int D, bool CAUSAL, bool VARLEN>
@@ -179,18 +194,17 @@ void prefill_kernel(PrefillParams p) {
   const int row_lim = VARLEN ? min(S, ((len + 63) / 64) * 64) : S;
 
   // This wave's slot and the workgroup's key range.
+  auto div_g = [&](int n) { return uniform(p.fast_div ? div_small(n, p.G, p.g_inv) : n / p.G); };
   const int slot = sg * kSlots + wave;
-  const int hl = slot % p.G;
-  const int r0 = (slot / p.G) * kRows;
+  const int slot_q = div_g(slot);
+  const int hl = slot - slot_q * p.G;
+  const int r0 = slot_q * kRows;
   const bool active = slot < p.G * p.n_rb && r0 < row_lim;
   int kv_end = S;
   if constexpr (CAUSAL) {
-    int last_r0 = 0;
-    for (int w = 0; w < kSlots; ++w) {
-      const int f = sg * kSlots + w;
-      if (f < p.G * p.n_rb) last_r0 = max(last_r0, (f / p.G) * kRows);
-    }
-    kv_end = min(row_lim, last_r0 + kRows);
+    // The workgroup's last valid slot has its largest row block.
+    const int f_last = min(sg * kSlots + kSlots - 1, p.G * p.n_rb - 1);
+    kv_end = min(row_lim, div_g(f_last) * kRows + kRows);
   }
   const int key_lim = (VARLEN && CAUSAL) ? len : S;  // rows at or past this are never staged
   const int n_tiles = uniform((kv_end + kBN - 1) / kBN);
@@ -545,14 +559,14 @@ void prefill_kernel(PrefillParams p) {
 }
 
 template <int D, bool CAUSAL, bool VARLEN>
-int launch(const PrefillParams& p, unsigned grid, hipStream_t st) {
+int launch(const PrefillParams& p, dim3 grid, hipStream_t st) {
   KernelTimer timer;
-  timer.launch(prefill_kernel<D, CAUSAL, VARLEN>, dim3(grid), dim3(kPThreads), 0, st, p);
+  timer.launch(prefill_kernel<D, CAUSAL, VARLEN>, grid, dim3(kPThreads), 0, st, p);
   return check_launch("prefill_kernel");
 }
 
 template <int D>
-int launch_d(bool causal, bool varlen, const PrefillParams& p, unsigned grid, hipStream_t st) {
+int launch_d(bool causal, bool varlen, const PrefillParams& p, dim3 grid, hipStream_t st) {
   if (causal) return varlen ? launch<D, true, true>(p, grid, st) : launch<D, true, false>(p, grid, st);
   return varlen ? launch<D, false, true>(p, grid, st) : launch<D, false, false>(p, grid, st);
 }
@@ -615,15 +629,19 @@ int prefill_impl(const void* q, const void* k, const void* v, void* o, float* ls
   p.S = (int)seq_len;
   p.n_rb = (int)ceil_div(seq_len, kRows);
   p.n_sg = (int)ceil_div((int64_t)p.G * p.n_rb, kSlots);
-  p.xcd_map = ((batch * num_kv_heads) % 8 == 0) ? 1 : 0;
+  p.grid1d = (batch > 65535 || p.n_sg > 65535) ? 1 : 0;
+  p.fast_div = ((int64_t)p.G * p.n_rb + kSlots < (1ll << 22)) ? 1 : 0;
+  p.g_inv = 1.0f / (float)p.G;
   p.qk_scale = softmax_scale * kLog2e;
-  const int64_t grid = batch * num_kv_heads * p.n_sg;
-  AKT_CHECK(grid < (1ll << 31), "problem too large");
+  const int64_t n_wg = batch * num_kv_heads * p.n_sg;
+  AKT_CHECK(n_wg < (1ll << 31), "problem too large");
+  const dim3 grid = p.grid1d ? dim3((unsigned)n_wg)
+                             : dim3((unsigned)num_kv_heads, (unsigned)batch, (unsigned)p.n_sg);
   const bool is_causal = causal != 0;
   const bool is_var = varlen != nullptr;
   hipStream_t st = (hipStream_t)stream;
-  if (head_dim == 64) return launch_d<64>(is_causal, is_var, p, (unsigned)grid, st);
-  return launch_d<128>(is_causal, is_var, p, (unsigned)grid, st);
+  if (head_dim == 64) return launch_d<64>(is_causal, is_var, p, grid, st);
+  return launch_d<128>(is_causal, is_var, p, grid, st);
 }
 }  // namespace
 
