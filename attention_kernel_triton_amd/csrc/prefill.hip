@@ -459,6 +459,14 @@ void prefill_kernel(PrefillParams p) {
 
     float l_step[2];
     softmax(scur, pcur, l_step);
+    // Issue order of the region: each of the 16 P.V / QK MFMAs followed by
+    // three VALU instructions, so one wave alternates its matrix and vector
+    // work instead of issuing them in clusters (2% per tile, measured).
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+      __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // three VALU
+    }
     bool over = false;
 #pragma unroll
     for (int rb = 0; rb < 2; ++rb) over |= !(l_step[rb] <= kStepSumLimit);
