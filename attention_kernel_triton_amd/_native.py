@@ -114,25 +114,41 @@ def ptr(t: torch.Tensor | None):
     return None if t is None else C.c_void_p(t.data_ptr())
 
 
+# torch's raw current-stream query (what Triton's launcher uses) skips building
+# a Stream object: ~0.2 us instead of ~1.8 us per call.
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_of(t: torch.Tensor):
-    return C.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+    """The current HIP stream of ``t``'s device, as a ctypes pointer."""
+    idx = t.device.index
+    if idx is None:
+        idx = torch.cuda.current_device()
+    if _raw_stream is not None:
+        return C.c_void_p(_raw_stream(idx))
+    return C.c_void_p(torch.cuda.current_stream(idx).cuda_stream)
 
 
 _WS_CACHE: dict = {}
 
 
-def workspace(nbytes: int, device) -> torch.Tensor | None:
-    """Decode workspace for the current stream of ``device``.
+def workspace(nbytes: int, device, stream=None) -> torch.Tensor | None:
+    """Decode workspace for ``stream`` (default: the current stream of ``device``).
 
     The C ABI requires the workspace's 256-byte counter header to be zero
     before first use (each call leaves it zero) and a workspace to be reused
     only by calls ordered on one stream, so one zero-initialised buffer is
-    kept per (device, stream) and grown when a call needs more.
+    kept per (device, stream) and grown when a call needs more.  ``stream`` is
+    the value ``stream_of`` returned for the same call.
     """
     if nbytes == 0:
         return None
     dev = torch.device(device)
-    key = (dev.index, torch.cuda.current_stream(dev).cuda_stream)
+    if dev.index is None:
+        dev = torch.device(dev.type, torch.cuda.current_device())
+    if stream is None:
+        stream = C.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+    key = (dev.index, stream.value)
     buf = _WS_CACHE.get(key)
     if buf is None or buf.numel() < nbytes:
         size = max(int(nbytes), 2 * buf.numel() if buf is not None else 0)

@@ -17,7 +17,7 @@ from . import _native as N
 def _need_gpu(name: str, t: torch.Tensor) -> None:
     if not isinstance(t, torch.Tensor):
         raise TypeError(f"{name} must be a torch.Tensor")
-    if t.device.type != "cuda":
+    if not t.is_cuda:
         raise ValueError(f"{name} must be on a ROCm GPU device, got {t.device}")
 
 
@@ -143,10 +143,11 @@ def decode(q, K, V, softmax_scale: float, return_lse: bool = False, chunk_tokens
     lse = torch.empty((B, Hq), dtype=torch.float32, device=q.device) if return_lse else None
     lib = N.load()
     ws_n = lib.akt_decode_workspace_size(B, Hq, Hkv, S, D, chunk_tokens)
-    ws = N.workspace(ws_n, q.device)
+    st = N.stream_of(q)
+    ws = N.workspace(ws_n, q.device, st)
     rc = lib.akt_decode_fwd(N.ptr(q), N.ptr(K), N.ptr(V), N.ptr(o), N.ptr(lse), B, Hq, Hkv, S, D,
                             N.strides(q), N.strides(K), N.strides(V), float(softmax_scale),
-                            chunk_tokens, N.ptr(ws), ws_n, N.stream_of(q))
+                            chunk_tokens, N.ptr(ws), ws_n, st)
     N.check(rc, "akt_decode_fwd")
     return (o, lse) if return_lse else o
 
@@ -176,11 +177,12 @@ def decode_paged(q, paged_kv_cache, kv_page_indptr, kv_page_indices, kv_last_pag
     total = indices.numel()
     lib = N.load()
     ws_n = lib.akt_decode_paged_workspace_size(B, Hq, Hkv, D, page, total, chunk_tokens)
-    ws = N.workspace(ws_n, dev)
+    st = N.stream_of(q)
+    ws = N.workspace(ws_n, dev, st)
     rc = lib.akt_decode_paged_fwd(N.ptr(q4), N.ptr(pool), N.ptr(indptr), N.ptr(indices),
                                   N.ptr(last), N.ptr(o), N.ptr(lse), B, Hq, Hkv, D, page, total,
                                   P, N.strides(q4), N.strides(pool), scale, chunk_tokens,
-                                  N.ptr(ws), ws_n, N.stream_of(q))
+                                  N.ptr(ws), ws_n, st)
     N.check(rc, "akt_decode_paged_fwd")
     return (o, lse) if return_lse else o
 
@@ -213,11 +215,12 @@ def sparse_decode(q, K, V, sparse_ind, sparse_nnz, softmax_scale: float,
     lse = torch.empty((B, Hq), dtype=torch.float32, device=dev) if return_lse else None
     lib = N.load()
     ws_n = lib.akt_sparse_decode_workspace_size(B, Hq, D, L, num_splits)
-    ws = N.workspace(ws_n, dev)
+    st = N.stream_of(q)
+    ws = N.workspace(ws_n, dev, st)
     rc = lib.akt_sparse_decode_fwd(N.ptr(q), N.ptr(K), N.ptr(V), N.ptr(ind), N.ptr(nnz),
                                    N.ptr(o), N.ptr(lse), B, Hq, Hkv, S, D, L, N.strides(q),
                                    N.strides(K), N.strides(V), ist, nst, float(softmax_scale),
-                                   num_splits, N.ptr(ws), ws_n, N.stream_of(q))
+                                   num_splits, N.ptr(ws), ws_n, st)
     N.check(rc, "akt_sparse_decode_fwd")
     return (o, lse) if return_lse else o
 
@@ -245,14 +248,15 @@ def sparse_decode_paged(q, paged_kv_cache, kv_page_indptr, kv_page_indices, spar
     lse = torch.empty((B, Hq), dtype=torch.float32, device=dev) if return_lse else None
     lib = N.load()
     ws_n = lib.akt_sparse_decode_workspace_size(B, Hq, D, L, num_splits)
-    ws = N.workspace(ws_n, dev)
+    st = N.stream_of(q)
+    ws = N.workspace(ws_n, dev, st)
     if lsh_k is None:
         scale = float(1.0 / math.sqrt(D)) if softmax_scale is None else float(softmax_scale)
         rc = lib.akt_sparse_decode_paged_fwd(N.ptr(q4), N.ptr(pool), N.ptr(indptr), N.ptr(indices),
                                              N.ptr(ind), N.ptr(nnz), N.ptr(o), N.ptr(lse), B, Hq,
                                              Hkv, D, page, P, L, N.strides(q4), N.strides(pool),
                                              ist, nst, scale, num_splits, N.ptr(ws), ws_n,
-                                             N.stream_of(q))
+                                             st)
         N.check(rc, "akt_sparse_decode_paged_fwd")
     else:
         for name, t in (("K", lsh_k), ("L", lsh_l)):
@@ -264,7 +268,7 @@ def sparse_decode_paged(q, paged_kv_cache, kv_page_indptr, kv_page_indices, spar
                                                N.ptr(indices), N.ptr(ind), N.ptr(nnz), N.ptr(lk),
                                                N.ptr(ll), N.ptr(o), N.ptr(lse), B, Hq, Hkv, D,
                                                page, P, L, N.strides(q4), N.strides(pool), ist,
-                                               nst, num_splits, N.ptr(ws), ws_n, N.stream_of(q))
+                                               nst, num_splits, N.ptr(ws), ws_n, st)
         N.check(rc, "akt_magicpig_decode_paged_fwd")
     return (o, lse) if return_lse else o
 
@@ -305,11 +309,12 @@ def sparse_decode_csr(q, K, V, inds, ptr, softmax_scale: float, return_lse: bool
     lse = torch.empty((B, Hq), dtype=torch.float32, device=dev) if return_lse else None
     lib = N.load()
     ws_n = lib.akt_sparse_decode_workspace_size(B, Hq, D, hint, num_splits)
-    ws = N.workspace(ws_n, dev)
+    st = N.stream_of(q)
+    ws = N.workspace(ws_n, dev, st)
     rc = lib.akt_sparse_decode_csr_fwd(N.ptr(q), N.ptr(K), N.ptr(V), N.ptr(inds), N.ptr(ptr),
                                        N.ptr(o), N.ptr(lse), B, Hq, Hkv, S, D, hint, N.strides(q),
                                        N.strides(K), N.strides(V), float(softmax_scale),
-                                       num_splits, N.ptr(ws), ws_n, N.stream_of(q))
+                                       num_splits, N.ptr(ws), ws_n, st)
     N.check(rc, "akt_sparse_decode_csr_fwd")
     return (o, lse) if return_lse else o
 
@@ -344,12 +349,13 @@ def sparse_decode_paged_csr(q, paged_kv_cache, kv_page_indptr, kv_page_indices, 
     lse = torch.empty((B, Hq), dtype=torch.float32, device=dev) if return_lse else None
     lib = N.load()
     ws_n = lib.akt_sparse_decode_workspace_size(B, Hq, D, hint, num_splits)
-    ws = N.workspace(ws_n, dev)
+    st = N.stream_of(q)
+    ws = N.workspace(ws_n, dev, st)
     rc = lib.akt_sparse_decode_paged_csr_fwd(N.ptr(q4), N.ptr(pool), N.ptr(indptr),
                                              N.ptr(indices), N.ptr(inds), N.ptr(ptr), N.ptr(lk),
                                              N.ptr(ll), N.ptr(o), N.ptr(lse), B, Hq, Hkv, D, page,
                                              P, hint, N.strides(q4), N.strides(pool), num_splits,
-                                             N.ptr(ws), ws_n, N.stream_of(q))
+                                             N.ptr(ws), ws_n, st)
     N.check(rc, "akt_sparse_decode_paged_csr_fwd")
     return (o, lse) if return_lse else o
 

@@ -172,3 +172,21 @@ def test_paged_repeated_calls_are_bit_identical(dev):
     from attention_kernel_triton_amd import _native
     for buf in _native._WS_CACHE.values():
         assert int(buf[:256].count_nonzero()) == 0
+
+
+def test_paged_on_a_side_stream_matches_the_default_stream(dev):
+    """Each stream gets its own workspace (its scheduling counters must not be shared
+    by calls that can overlap), and the kernels launch on the caller's current stream."""
+    from attention_kernel_triton_amd import _native
+    p = syn.paged_config(B=8, min_len=256, max_len=3000).to(dev)
+    ref = pg.flash_attention_decode_paged(p.q, p.pool, p.indptr, p.indices, p.last_len)
+    side = torch.cuda.Stream(device=dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(side):
+        o = pg.flash_attention_decode_paged(p.q, p.pool, p.indptr, p.indices, p.last_len)
+        key = (torch.device(dev).index or 0, side.cuda_stream)
+    torch.cuda.synchronize(dev)
+    assert torch.equal(o, ref)
+    assert key in _native._WS_CACHE
+    # ctypes reads the null (default) stream back as None
+    assert (_native.stream_of(p.q).value or 0) == torch.cuda.current_stream(dev).cuda_stream
