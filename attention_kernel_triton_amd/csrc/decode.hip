@@ -38,9 +38,9 @@ enum : int { kModeDense = 0, kModePaged = 1, kModeSparseDense = 2, kModeSparsePa
 
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / kWave;
-// Split-KV chunk lengths (tokens) of dense and paged caches: 2, 4 or 8
-// 16-token groups per wave.
-constexpr int kMaxChunk = 512;
+// Split-KV chunk lengths (tokens) of dense and paged caches: 128, 256, 512 or
+// 640, i.e. 2, 4, 8 or 10 16-token groups per wave.
+constexpr int kMaxChunk = 640;
 // Largest batch whose paged chunk table fits the persistent kernel's LDS.
 constexpr int kMaxTableB = 1024;
 constexpr int kMaxDevices = 64;
@@ -339,7 +339,7 @@ __global__ __launch_bounds__(kThreads) void split_kernel(SplitParams p) {
   // Query fragment (B operand): head hq0 + c16, dims R*KPL + 8s + e.  For paged
   // caches with page_size % 16 == 0 (one page per 16-token group), lane k
   // prefetches the page id and slot of this wave's k-th group (a chunk has at
-  // most kMaxChunk tokens, so at most 8 groups per wave).
+  // most kMaxChunk tokens, so at most 10 groups per wave).
   auto setup = [&](const Item& w, IssueCtx& cx, half8_t (&qd)[KS]) {
     const int64_t k_unit = PAGED_ADDR ? (int64_t)w.kvh * p.k_head
                                       : (int64_t)w.b * p.k_batch + (int64_t)w.kvh * p.k_head;
@@ -1005,6 +1005,7 @@ int launch_t(const SplitParams& p, dim3 grid, dim3 cgrid, hipStream_t st) {
       if (!persist) {
       } else if (p.chunk == 128) rc = launch_split<D, GT, MODE, ALIGNED, MAGIC, 2, true>(p, grid, st);
       else if (p.chunk == 256) rc = launch_split<D, GT, MODE, ALIGNED, MAGIC, 4, true>(p, grid, st);
+      else if (p.chunk == 640) rc = launch_split<D, GT, MODE, ALIGNED, MAGIC, 10, true>(p, grid, st);
       else rc = launch_split<D, GT, MODE, ALIGNED, MAGIC, 8, true>(p, grid, st);
     }
     if (rc) return rc;
@@ -1044,21 +1045,27 @@ int launch_d(int D, int gt, const SplitParams& p, dim3 grid, dim3 cgrid, hipStre
   return set_error(AKT_ERR_UNSUPPORTED, "head_dim %d not supported (64, 128, 256)", D);
 }
 
-// Automatic chunk length for dense / paged caches: the smallest supported
-// length (128, 256, 512) that keeps the item count near 4096.
-// Smallest supported chunk that cuts the launch into at most ~256 items
-// (in practice the largest chunk unless the launch is tiny): an item carries a
-// fixed cost (startup latency, the workgroup merge, a partial) that small
-// chunks do not amortise -- measured on MI355X, 512-token chunks beat 128 and
-// 256 both for config 3 (paged, ~1900 items) and config 2 (dense, 256 items).
+// Automatic chunk length for dense / paged caches.  An item carries a fixed
+// cost (the workgroup merge, a partial, its share of the combine) that small
+// chunks do not amortise, while the last items set the launch's tail:
+// - the smallest of 128, 256 and 512 that cuts the launch into at most ~256
+//   items (in practice 512 unless the launch is tiny): measured on MI355X,
+//   512 beats 128 and 256 for config 2 (dense, 256 items) and config 3;
+// - 640 when even a lower bound on its item count (total tokens / 640 per
+//   unit) leaves each of the ~512 resident workgroups (two per CU) at least
+//   2.75 items.  Config 3 (paged, 1569 items), nine in-process pairs on
+//   three MI355X boxes: 92.3-94.4 us against 94.0-96.7 at 512 (mean -1.2 us);
+//   768-token chunks (2.6 items per workgroup) took 97-98 us.
 int64_t auto_chunk(int64_t total_tokens, int64_t units) {
+  constexpr int64_t kResidentWorkgroups = 512;
+  if ((total_tokens / 640) * units * 4 >= kResidentWorkgroups * 11) return 640;
   const int64_t want = ceil_div(total_tokens * units, 256);
   int64_t c = 128;
-  while (c < want && c < kMaxChunk) c <<= 1;
+  while (c < want && c < 512) c <<= 1;
   return c;
 }
 
-bool chunk_ok(int64_t c) { return c == 0 || c == 128 || c == 256 || c == 512; }
+bool chunk_ok(int64_t c) { return c == 0 || c == 128 || c == 256 || c == 512 || c == 640; }
 
 // Chunk length of a paged launch: pages that do not hold whole 16-token
 // groups and batches past the LDS chunk table use 256-token chunks.
@@ -1123,7 +1130,7 @@ extern "C" int akt_decode_fwd(const void* q, const void* k, const void* v, void*
   AKT_CHECK(rows_aligned16(q, q_stride, 3) && rows_aligned16(k, k_stride, 3) &&
                 rows_aligned16(v, v_stride, 3) && aligned16(o),
             "tensors must have 16-byte aligned rows");
-  AKT_CHECK(chunk_ok(chunk_tokens), "chunk_tokens must be 0 (automatic), 128, 256 or 512");
+  AKT_CHECK(chunk_ok(chunk_tokens), "chunk_tokens must be 0 (automatic), 128, 256, 512 or 640");
   if (batch == 0) return AKT_OK;
   const int D = (int)head_dim;
   const int G = (int)(num_q_heads / num_kv_heads);
@@ -1200,7 +1207,7 @@ extern "C" int akt_decode_paged_fwd(const void* q, const void* kv_cache,
   AKT_CHECK(q_stride[3] == 1 && kv_stride[4] == 1, "head_dim stride must be 1");
   AKT_CHECK(rows_aligned16(q, q_stride, 3) && rows_aligned16(kv_cache, kv_stride, 4) && aligned16(o),
             "tensors must have 16-byte aligned rows");
-  AKT_CHECK(chunk_ok(chunk_tokens), "chunk_tokens must be 0 (automatic), 128, 256 or 512");
+  AKT_CHECK(chunk_ok(chunk_tokens), "chunk_tokens must be 0 (automatic), 128, 256, 512 or 640");
   if (batch == 0) return AKT_OK;
   const int D = (int)head_dim;
   const int G = (int)(num_q_heads / num_kv_heads);

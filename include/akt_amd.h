@@ -130,7 +130,7 @@ int akt_merge_states(const void* o_parts, int o_parts_dtype, const float* lse_pa
  *   o: contiguous [batch, num_q_heads, head_dim] fp16;
  *   lse: optional contiguous [batch, num_q_heads] fp32 (natural log of the
  *   softmax normaliser of the scaled scores).  head_dim: 64, 128 or 256.
- *   chunk_tokens: split-KV chunk length: 128, 256 or 512 tokens, 0 = automatic
+ *   chunk_tokens: split-KV chunk length: 128, 256, 512 or 640 tokens, 0 = automatic
  *   (a hint: pages that do not hold whole 16-token groups, and paged batches
  *   over 1024 sequences, use 256).
  */

@@ -89,6 +89,23 @@ def test_workspace_sizes_scale_with_problem():
     assert lib.akt_sparse_decode_workspace_size(1, 32, 128, 3840, 8) == 256 + 32 * 8 * 132 * 4
 
 
+def test_automatic_chunk_length():
+    """The automatic split-KV chunk: 640 tokens once a launch leaves each of ~512
+    resident workgroups at least 2.75 items at that length, else the smallest of
+    128/256/512 that cuts it into at most ~256 items.  The workspace size is a
+    function of the chunk, so it shows the choice."""
+    lib = N.load()
+    ws = lib.akt_decode_paged_workspace_size
+    # config 3: 7208 pages of 16 tokens, 8 kv heads -> 640-token chunks
+    assert ws(32, 32, 8, 128, 16, 7208, 0) == ws(32, 32, 8, 128, 16, 7208, 640)
+    assert ws(32, 32, 8, 128, 16, 7208, 0) != ws(32, 32, 8, 128, 16, 7208, 512)
+    # a smaller pool stays at 512
+    assert ws(32, 32, 8, 128, 16, 5000, 0) == ws(32, 32, 8, 128, 16, 5000, 512)
+    # config 2 (dense, 8 x 1024 tokens, 16 kv heads) stays at 512
+    dws = lib.akt_decode_workspace_size
+    assert dws(8, 64, 16, 1024, 64, 0) == dws(8, 64, 16, 1024, 64, 512)
+
+
 def test_kept_index_rejects_short_row_stride():
     lib = N.load()
     rc = lib.akt_kept_index_from_mask(C.c_void_p(16), 4, 100, 50, None, C.c_void_p(16), 10,

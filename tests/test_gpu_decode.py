@@ -36,7 +36,7 @@ def test_decode_shapes(dev, D, G, S):
     assert_close(lse, rl, atol=1e-4, what="decode lse")
 
 
-@pytest.mark.parametrize("chunk", [128, 256, 512])
+@pytest.mark.parametrize("chunk", [128, 256, 512, 640])
 def test_decode_chunking_does_not_change_results(dev, chunk):
     q, K, V = _dec_inputs(3, 2, 4, 4, 777, 128)
     o, lse = _ops.decode(q.to(dev), K.to(dev), V.to(dev), 0.09, return_lse=True,
@@ -131,6 +131,17 @@ def test_paged_config3_full(dev):
     err = assert_close(o, ro, what="config 3")
     assert_close(lse, rl, atol=1e-4, what="config 3 lse")
     print(f"config 3 max abs err {err:.3e}")
+
+
+@pytest.mark.parametrize("chunk", [256, 512, 640])
+def test_paged_chunk_lengths(dev, chunk):
+    p = syn.paged_config(B=8, min_len=1, max_len=5000)
+    d = p.to(dev)
+    o, lse = _ops.decode_paged(d.q, d.pool, d.indptr, d.indices, d.last_len, return_lse=True,
+                               chunk_tokens=chunk)
+    ro, rl = naive.naive_paged_attention(p.q, p.pool, p.indptr, p.indices, p.last_len)
+    assert_close(o, ro, what=f"paged chunk {chunk}")
+    assert_close(lse, rl, atol=1e-4, what=f"paged chunk {chunk} lse")
 
 
 def test_paged_config3_page_relabelling_is_bit_exact(dev):
