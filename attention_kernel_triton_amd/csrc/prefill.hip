@@ -200,6 +200,13 @@ void prefill_kernel(PrefillParams p) {
   const int hl = slot - slot_q * p.G;
   const int r0 = slot_q * kRows;
   const bool active = slot < p.G * p.n_rb && r0 < row_lim;
+  // Var-len: slots, and with them their row blocks, grow with the wave index,
+  // so when the first slot's rows start past ceil(len / 64) * 64 no wave of
+  // the workgroup has a row to compute, and it leaves before staging any tile
+  // (workgroup-uniform).
+  if constexpr (VARLEN) {
+    if (div_g(sg * kSlots) * kRows >= row_lim) return;
+  }
   int kv_end = S;
   if constexpr (CAUSAL) {
     // The workgroup's last valid slot has its largest row block.

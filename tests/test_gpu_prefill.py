@@ -97,6 +97,24 @@ def test_prefill_varlen_nonfinite_padding_never_leaks(dev, bits):
     assert_close(out, ref, what="var-len padding", mask=valid)
 
 
+@pytest.mark.parametrize("G", [1, 3, 4, 8])
+@pytest.mark.parametrize("D", [64, 128])
+def test_prefill_varlen_block_edges_and_idle_workgroups(dev, G, D):
+    """Lengths at and around 64-row block edges, an empty sequence and a full one:
+    workgroups whose row blocks all lie past ceil(len / 64) * 64 exit at once, and
+    with G != 4 one workgroup mixes active and idle waves."""
+    Hkv, S = 2, 320
+    lens = torch.tensor([0, 1, 63, 64, 65, 200, 320])
+    B = len(lens)
+    Q, K, V = _qkv(13 + G + D, B, Hkv * G, Hkv, S, D)
+    out = prevar.flash_attention_prefill(Q.to(dev), K.to(dev), V.to(dev), True, 1 / math.sqrt(D),
+                                         G, varlen=lens.to(dev)).cpu()
+    ref = naive.prefill_varlen(Q, K, V, True, 1 / math.sqrt(D), G, lens)
+    valid = (torch.arange(S)[None, :] < lens[:, None])[:, None, :, None].expand(Q.shape)
+    assert torch.isfinite(out[valid]).all()
+    assert_close(out, ref, what=f"var-len edges G={G} D={D}", mask=valid)
+
+
 def test_prefill_varlen_noncausal_matches_reference_semantics(dev):
     """Non-causal var-len attends all S keys, padding included (reference behaviour)."""
     B, Hq, Hkv, S, D = 2, 2, 1, 130, 64
