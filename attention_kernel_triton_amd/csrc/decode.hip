@@ -401,7 +401,7 @@ __global__ __launch_bounds__(kThreads) void split_kernel(SplitParams p) {
       ra = pos_k;
     } else if constexpr (MODE == kModePaged) {
       if constexpr (ALIGNED) {
-        const int k = (g - cx.g_begin - wave) >> 2;
+        const int k = (g - cx.g_begin - wave) / kWaves;
         const int page = __builtin_amdgcn_readlane(cx.page_pref, k);
         gslot = __builtin_amdgcn_readlane(cx.slot_pref, k);
         const bool page_ok = page >= 0 && page < p.num_pool_pages;
