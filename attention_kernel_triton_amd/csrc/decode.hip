@@ -1056,8 +1056,11 @@ int launch_d(int D, int gt, const SplitParams& p, dim3 grid, dim3 cgrid, hipStre
 //   2.75 items.  Config 3 (paged, 1569 items), nine in-process pairs on
 //   three MI355X boxes: 92.3-94.4 us against 94.0-96.7 at 512 (mean -1.2 us);
 //   768-token chunks (2.6 items per workgroup) took 97-98 us.
+// Workgroups of the decode kernels resident at once on MI355X: two per CU
+// (VGPR-bound) on 256 CUs.
+constexpr int64_t kResidentWorkgroups = 512;
+
 int64_t auto_chunk(int64_t total_tokens, int64_t units) {
-  constexpr int64_t kResidentWorkgroups = 512;
   if ((total_tokens / 640) * units * 4 >= kResidentWorkgroups * 11) return 640;
   const int64_t want = ceil_div(total_tokens * units, 256);
   int64_t c = 128;
@@ -1075,8 +1078,16 @@ int64_t paged_chunk(int64_t chunk_tokens, int64_t total_pages, int64_t page_size
   return chunk_tokens > 0 ? chunk_tokens : auto_chunk(total_pages * page_size, Y);
 }
 
+// Automatic split count of sparse rows: as many splits per row as fit one
+// round of resident workgroups, at most one per 64 index slots.  A sparse
+// workgroup is a chain of dependent round trips (nnz, page table, indices,
+// page ids, rows) whatever its token count, so a second round of workgroups
+// costs a whole second chain.  Measured on MI355X (split kernel):
+//   config 4a (32 rows):  32 splits 10.5-11.0 us, 16 splits 6.9-7.9 us;
+//   config 4b (96 rows):  11 splits 20.3-20.5 us, 5 splits 16.8 us;
+//   MagicPIG 4b:          11 splits 26.6 us,      5 splits 23.8 us.
 int64_t auto_splits(int64_t rows, int64_t l_max) {
-  int64_t s = ceil_div(1024, rows > 0 ? rows : 1);
+  int64_t s = kResidentWorkgroups / (rows > 0 ? rows : 1);
   const int64_t cap = ceil_div(l_max > 0 ? l_max : 1, 64);
   if (s > cap) s = cap;
   return s < 1 ? 1 : s;
