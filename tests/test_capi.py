@@ -106,6 +106,18 @@ def test_automatic_chunk_length():
     assert dws(8, 64, 16, 1024, 64, 0) == dws(8, 64, 16, 1024, 64, 512)
 
 
+def test_automatic_sparse_split_count():
+    """Sparse rows get as many splits as fit one round of ~512 resident workgroups,
+    at most one per 64 index slots of l_max; the workspace size shows the count."""
+    lib = N.load()
+    ws = lib.akt_sparse_decode_workspace_size
+    part = lambda rows, ns, D: 256 + rows * ns * (D + 4) * 4
+    assert ws(1, 32, 128, 3840, 0) == part(32, 16, 128)      # config 4a: 512 / 32 rows
+    assert ws(3, 32, 256, 32768, 0) == part(96, 5, 256)      # config 4b: 512 / 96 rows
+    assert ws(1, 32, 128, 200, 0) == part(32, 4, 128)        # capped at ceil(200 / 64)
+    assert ws(64, 32, 128, 3840, 0) == 256                   # 2048 rows: one split, no partials
+
+
 def test_kept_index_rejects_short_row_stride():
     lib = N.load()
     rc = lib.akt_kept_index_from_mask(C.c_void_p(16), 4, 100, 50, None, C.c_void_p(16), 10,
