@@ -117,15 +117,21 @@ def _cpu_model():
     return "unknown CPU"
 
 
-def _cpu_time(fn, reps):
+CPU_BUDGET_S = 10.0  # CPU work per baseline: at least 3 runs, then runs until this is spent
+
+
+def _cpu_time(fn, min_reps=3, budget_s=CPU_BUDGET_S):
+    """Median wall time of fn over runs totalling about budget_s (after a warm-up);
+    returns (median seconds, runs, total seconds)."""
     fn()  # warm-up
     ts = []
-    for _ in range(reps):
+    while len(ts) < min_reps or sum(ts) < budget_s:
         t0 = time.perf_counter()
         fn()
         ts.append(time.perf_counter() - t0)
+    total = sum(ts)
     ts.sort()
-    return ts[len(ts) // 2]
+    return ts[len(ts) // 2], len(ts), total
 
 
 def bench_paged(args):
@@ -159,13 +165,13 @@ def bench_paged(args):
         from oracle import naive
         _log("CPU baseline: oracle naive_paged_attention (fp32) on config 3")
         torch.set_num_threads(_cpu_threads())
-        reps = 3
-        t = _cpu_time(lambda: naive.naive_paged_attention(
-            cfg.q, cfg.pool, cfg.indptr, cfg.indices, cfg.last_len, dtype=torch.float32), reps)
+        t, reps, total = _cpu_time(lambda: naive.naive_paged_attention(
+            cfg.q, cfg.pool, cfg.indptr, cfg.indices, cfg.last_len, dtype=torch.float32))
         out["cpu_baseline"] = {"value": nbytes / t / 1e9, "unit": "GB/s",
                                "cores": torch.get_num_threads(), "kind": "port",
                                "sample": f"full config 3 batch, median of {reps} runs "
-                                         f"({t * 1e3:.0f} ms each), fp32 torch on "
+                                         f"({t * 1e3:.0f} ms each, {total:.1f} s in all), "
+                                         f"fp32 torch on "
                                          f"{torch.get_num_threads()} threads of {_cpu_model()}"}
     del p
     return out
@@ -202,13 +208,13 @@ def bench_prefill(args):
         _log("CPU baseline: oracle prefill (fp32) on 2 of 8 batches of config 0")
         torch.set_num_threads(_cpu_threads())
         nb = 2
-        reps = 3
-        t = _cpu_time(lambda: naive.prefill(cfg.Q[:nb], cfg.K[:nb], cfg.V[:nb], True, cfg.scale,
-                                            cfg.group, dtype=torch.float32), reps)
+        t, reps, total = _cpu_time(lambda: naive.prefill(
+            cfg.Q[:nb], cfg.K[:nb], cfg.V[:nb], True, cfg.scale, cfg.group, dtype=torch.float32))
         out["cpu_baseline"] = {"value": flops * nb / 8 / t / 1e12, "unit": "TFLOP/s",
                                "cores": torch.get_num_threads(), "kind": "port",
                                "sample": f"2 of 8 batches of config 0, median of {reps} runs "
-                                         f"({t * 1e3:.0f} ms each), fp32 torch on "
+                                         f"({t * 1e3:.0f} ms each, {total:.1f} s in all), "
+                                         f"fp32 torch on "
                                          f"{torch.get_num_threads()} threads of {_cpu_model()}"}
     return out
 
