@@ -507,22 +507,33 @@ __global__ __launch_bounds__(kThreads) void split_kernel(SplitParams p) {
 
     float t[4];
     if constexpr (MAGIC) {
-      // |k|^2 of token c16 (K-lane layout), then fetch for tokens 4R + r.
+      // A sparse unit is one head (column 0 of the score tile), so the group
+      // needs 16 corrections, one per token: lane l evaluates token l & 15
+      // (its dot product comes from lane 16 (tt / 4), register tt % 4, and
+      // |k|^2 from the K-lane layout), and each score lane then fetches the
+      // scores of its tokens 4R + r.  Lanes of columns past the head carry
+      // head 0's scores, which are never stored.
       float ks = 0.f;
 #pragma unroll
       for (int s = 0; s < KS; ++s)
 #pragma unroll
         for (int j = 0; j < 4; ++j) ks = dot2(bf.k[s][j], bf.k[s][j], ks);
       ks = rows_sum(ks);
+      const int tt = lane & 15;
+      const int src = (tt >> 2) << 4;
+      const float d0 = __shfl(sacc[0], src, 64), d1 = __shfl(sacc[1], src, 64);
+      const float d2 = __shfl(sacc[2], src, 64), d3 = __shfl(sacc[3], src, 64);
+      const int rr = tt & 3;
+      const float dotp = rr == 0 ? d0 : (rr == 1 ? d1 : (rr == 2 ? d2 : d3));
+      const float kn = sqrtf(__shfl(ks, tt, 64));
+      const float qn = __shfl(q_norm, 0, 64);  // |q| of the unit's head (lane 0)
+      float cosv = dotp / (qn * kn + 1e-8f);
+      cosv = fminf(fmaxf(cosv, -1.0f + 1e-7f), 1.0f - 1e-7f);
+      const float sc_t = dotp * p.inv_sqrt_d - magicpig_log_u(cosv, lsh_k, lsh_l);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int tt = 4 * R + r;
-        const float kn = sqrtf(__shfl(ks, tt, 64));
-        const float dotp = sacc[r];
-        float cosv = dotp / (q_norm * kn + 1e-8f);
-        cosv = fminf(fmaxf(cosv, -1.0f + 1e-7f), 1.0f - 1e-7f);
-        const float sc = dotp * p.inv_sqrt_d - magicpig_log_u(cosv, lsh_k, lsh_l);
-        t[r] = ((vmask >> tt) & 1) ? sc * kLog2e : AKT_NEG_INF;
+        const float sc = __shfl(sc_t, 4 * R + r, 64);
+        t[r] = ((vmask >> (4 * R + r)) & 1) ? sc * kLog2e : AKT_NEG_INF;
       }
     } else {
 #pragma unroll
