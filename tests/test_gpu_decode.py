@@ -201,3 +201,28 @@ def test_paged_on_a_side_stream_matches_the_default_stream(dev):
     assert key in _native._WS_CACHE
     # ctypes reads the null (default) stream back as None
     assert (_native.stream_of(p.q).value or 0) == torch.cuda.current_stream(dev).cuda_stream
+
+
+def test_paged_on_two_streams_at_once(dev):
+    """Two launches in flight together on two streams: each stream has its own
+    workspace, so their scheduling counters never mix."""
+    p = syn.paged_config(B=16, min_len=256, max_len=6000).to(dev)
+    q2 = p.q.flip(1).contiguous()
+    ref1 = pg.flash_attention_decode_paged(p.q, p.pool, p.indptr, p.indices, p.last_len)
+    ref2 = pg.flash_attention_decode_paged(q2, p.pool, p.indptr, p.indices, p.last_len)
+    s1, s2 = torch.cuda.Stream(device=dev), torch.cuda.Stream(device=dev)
+    s1.wait_stream(torch.cuda.current_stream(dev))
+    s2.wait_stream(torch.cuda.current_stream(dev))
+    outs1, outs2 = [], []
+    for _ in range(4):
+        with torch.cuda.stream(s1):
+            outs1.append(pg.flash_attention_decode_paged(p.q, p.pool, p.indptr, p.indices,
+                                                         p.last_len))
+        with torch.cuda.stream(s2):
+            outs2.append(pg.flash_attention_decode_paged(q2, p.pool, p.indptr, p.indices,
+                                                         p.last_len))
+    torch.cuda.synchronize(dev)
+    for o in outs1:
+        assert torch.equal(o, ref1)
+    for o in outs2:
+        assert torch.equal(o, ref2)
