@@ -226,3 +226,38 @@ def test_paged_on_two_streams_at_once(dev):
         assert torch.equal(o, ref1)
     for o in outs2:
         assert torch.equal(o, ref2)
+
+
+def test_paged_page_ids_past_32_bit_byte_offsets(dev):
+    """Pages near the end of a 4.6 GB pool: page id x page stride overflows 32 bits, so
+    the row address must be formed in 64 bits.  Only the used pages are filled; the
+    oracle runs on a compact copy of them."""
+    Hq, Hkv, page, D = 8, 8, 16, 128
+    P = 70000  # 70000 pages x 2 x 8 x 16 x 128 x 2 B = 4.6 GB
+    lens = [100, 37]
+    npg = [(L + page - 1) // page for L in lens]
+    used = torch.arange(P - 1, P - 1 - sum(npg), -1, dtype=torch.int32)  # highest ids first
+    g = torch.Generator().manual_seed(21)
+    content = torch.randn(len(used), 2, Hkv, page, D, generator=g).half()
+    q = torch.randn(len(lens), Hq, 1, D, generator=g).half()
+    pool = torch.empty(P, 2, Hkv, page, D, dtype=torch.float16, device=dev)
+    pool[used.long().to(dev)] = content.to(dev)
+    indptr = torch.tensor([0, npg[0], npg[0] + npg[1]], dtype=torch.int32)
+    last = torch.tensor([L - (n - 1) * page for L, n in zip(lens, npg)], dtype=torch.int32)
+    o, lse = pg.flash_attention_decode_paged(q.to(dev), pool, indptr.to(dev), used.to(dev),
+                                             last.to(dev), return_lse=True)
+    compact = torch.arange(len(used), dtype=torch.int32)
+    ro, rl = naive.naive_paged_attention(q, content, indptr, compact, last)
+    assert_close(o, ro, what="paged, page ids near 70000")
+    assert_close(lse, rl, atol=1e-4, what="paged lse, page ids near 70000")
+    del pool
+
+
+def test_decode_long_sequence(dev):
+    """One 131072-token cache (four 640-token-or-less chunk rounds per unit and more)."""
+    q, K, V = _dec_inputs(22, 1, 2, 4, 131072, 128)
+    o, lse = dec.flash_attention_decode(q.to(dev), K.to(dev), V.to(dev), 1 / math.sqrt(128), 4,
+                                        return_lse=True)
+    ro, rl = naive.decode(q, K, V, 1 / math.sqrt(128), 4)
+    assert_close(o, ro, what="decode S=131072")
+    assert_close(lse, rl, atol=1e-4, what="decode S=131072 lse")

@@ -204,3 +204,33 @@ def test_magicpig_empty_head_and_L1_reduction(dev):
     ro, rl = naive.sparsetoken_naive_paged_attention(p.q, p.pool, p.indptr, p.indices, ind, nnz)
     assert_close(o, ro, what="MagicPIG L=1 == plain sparse")
     assert_close(lse[0, 1:], rl[0, 1:] - math.log(1e-10), atol=1e-3, what="L=1 lse shift")
+
+
+def test_sparse_paged_page_ids_past_32_bit_byte_offsets(dev):
+    """Kept tokens on pages near the end of a 4.6 GB pool (64-bit row addresses)."""
+    Hq, Hkv, page, D, P, L = 8, 8, 16, 128, 70000, 200
+    npg = (L + page - 1) // page
+    used = torch.arange(P - 1, P - 1 - npg, -1, dtype=torch.int32)
+    g = torch.Generator().manual_seed(23)
+    content = torch.randn(npg, 2, Hkv, page, D, generator=g).half()
+    q = torch.randn(1, Hq, 1, D, generator=g).half()
+    pool = torch.empty(P, 2, Hkv, page, D, dtype=torch.float16, device=dev)
+    pool[used.long().to(dev)] = content.to(dev)
+    indptr = torch.tensor([0, npg], dtype=torch.int32)
+    keep = torch.rand(1, Hq, L, generator=g) < 0.1
+    keep[..., L - 1] = True  # the last token lives on the highest page of the sequence
+    l_max = int(keep.sum(-1).max())
+    ind = torch.full((1, Hq, l_max), -1, dtype=torch.int32)
+    nnz = torch.zeros(1, Hq, 1, dtype=torch.int32)
+    for h in range(Hq):
+        idx = keep[0, h].nonzero().flatten().to(torch.int32)
+        ind[0, h, : len(idx)] = idx
+        nnz[0, h, 0] = len(idx)
+    o, lse = spp.sparsetoken_flash_attention_decode_paged(q.to(dev), pool, indptr.to(dev),
+                                                          used.to(dev), ind.to(dev), nnz.to(dev),
+                                                          return_lse=True)
+    compact = torch.arange(npg, dtype=torch.int32)
+    ro, rl = naive.sparsetoken_naive_paged_attention(q, content, indptr, compact, ind, nnz)
+    assert_close(o, ro, what="sparse paged, page ids near 70000")
+    assert_close(lse, rl, atol=1e-4, what="sparse paged lse, page ids near 70000")
+    del pool
