@@ -179,3 +179,13 @@ def test_prefill_nan_query_row_leaves_rows_outside_its_pair_exact(dev):
     keep[0, 1, (bad & ~31) + ((bad & 31) ^ 16)] = False
     assert torch.isfinite(out[keep]).all()
     assert_close(out, ref, what="rows outside the NaN row's pair", mask=keep)
+
+
+@pytest.mark.parametrize("D", [64, 128])
+def test_prefill_long_sequence(dev, D):
+    """An 8192-token causal sequence (128 key tiles per row block at the end)."""
+    B, Hq, Hkv, S = 1, 2, 1, 8192
+    Q, K, V = _qkv(31 + D, B, Hq, Hkv, S, D)
+    out = pre.flash_attention_prefill(Q.to(dev), K.to(dev), V.to(dev), True, 1 / math.sqrt(D), 2)
+    ref = naive.prefill(Q, K, V, True, 1 / math.sqrt(D), 2, dtype=torch.float32)
+    assert_close(out, ref, what=f"prefill S=8192 D={D}")
