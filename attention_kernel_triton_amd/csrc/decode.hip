@@ -1056,6 +1056,10 @@ int launch_d(int D, int gt, const SplitParams& p, dim3 grid, dim3 cgrid, hipStre
   return set_error(AKT_ERR_UNSUPPORTED, "head_dim %d not supported (64, 128, 256)", D);
 }
 
+// Workgroups of the decode kernels resident at once on MI355X: two per CU
+// (VGPR-bound) on 256 CUs.
+constexpr int64_t kResidentWorkgroups = 512;
+
 // Automatic chunk length for dense / paged caches.  An item carries a fixed
 // cost (the workgroup merge, a partial, its share of the combine) that small
 // chunks do not amortise, while the last items set the launch's tail:
@@ -1067,10 +1071,6 @@ int launch_d(int D, int gt, const SplitParams& p, dim3 grid, dim3 cgrid, hipStre
 //   2.75 items.  Config 3 (paged, 1569 items), nine in-process pairs on
 //   three MI355X boxes: 92.3-94.4 us against 94.0-96.7 at 512 (mean -1.2 us);
 //   768-token chunks (2.6 items per workgroup) took 97-98 us.
-// Workgroups of the decode kernels resident at once on MI355X: two per CU
-// (VGPR-bound) on 256 CUs.
-constexpr int64_t kResidentWorkgroups = 512;
-
 int64_t auto_chunk(int64_t total_tokens, int64_t units) {
   if ((total_tokens / 640) * units * 4 >= kResidentWorkgroups * 11) return 640;
   const int64_t want = ceil_div(total_tokens * units, 256);
