@@ -285,6 +285,9 @@ def _csr_meta(inds, ptr, dev, rows):
         raise ValueError(f"ptr must be [B*Hq + 1] = [{rows + 1}], got {tuple(ptr.shape)}")
     if inds.dim() != 1:
         raise ValueError("inds must be 1-D")
+    if inds.numel() == 0:
+        # Every row is empty; the C ABI still takes a valid pointer (never read).
+        inds = torch.full((1,), -1, dtype=torch.int32, device=dev)
     return inds, ptr.contiguous()
 
 

@@ -20,7 +20,10 @@ LIB_NAME = "libakt_amd.so"
 LIB_PATH = PKG_DIR / LIB_NAME
 ARCH = "gfx950"
 
-# Packed FP32 instructions are switched off for all device code.
+# Packed FP32 instructions are switched off for all device code.  The atomic
+# optimizer is off: every atomic here is issued by one lane, and the optimizer's
+# rewrite of a uniform-address atomic reads the returned value at once, which
+# makes the wave wait (vmcnt(0)) for every load it has in flight.
 COMMON_FLAGS = [
     f"--offload-arch={ARCH}",
     "-O3",
@@ -30,6 +33,7 @@ COMMON_FLAGS = [
     "-Wno-unused-function",
     "-Wno-pass-failed",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-mllvm", "-amdgpu-atomic-optimizer-strategy=None",
 ]
 
 

@@ -120,6 +120,8 @@ __device__ __forceinline__ uint32_t pair_hi(uint32_t a, uint32_t b) {
 
 __device__ __forceinline__ half8_t as_half8(uint4_t u) { return __builtin_bit_cast(half8_t, u); }
 __device__ __forceinline__ uint4_t as_uint4(half8_t h) { return __builtin_bit_cast(uint4_t, h); }
+__device__ __forceinline__ float4_t as_float4u(uint4_t u) { return __builtin_bit_cast(float4_t, u); }
+__device__ __forceinline__ uint4_t as_uint4f(float4_t f) { return __builtin_bit_cast(uint4_t, f); }
 
 // 16-byte global load / store.
 __device__ __forceinline__ uint4_t ld16(const void* p) {
@@ -129,5 +131,28 @@ __device__ __forceinline__ void st16(void* p, uint4_t v) { *reinterpret_cast<uin
 
 // Readfirstlane for 32-bit ints: moves a wave-uniform value into an SGPR.
 __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+// ---------------------------------------------------------------------------
+// Device-coherent 16-byte accesses through a raw buffer resource.
+// ---------------------------------------------------------------------------
+// Word 3 of a raw (stride 0) gfx9 buffer resource: 32-bit data format.
+constexpr int kBufferWord3 = 0x00020000;
+// Cache-policy operand of the buffer intrinsics: the device-scope bit (sc1).
+// A device-scope store is acknowledged only once it is visible to every CU of
+// the device, whichever XCD (and L2) it belongs to; a device-scope load never
+// returns a line that another XCD's L2 has made stale.  These are the
+// accesses the compiler emits for relaxed agent-scope atomics, here 16 bytes
+// wide.
+constexpr int kScopeDevice = 16;
+
+// 16-byte device-scope store / load at byte offset `off` (< 2^31) from `base`.
+__device__ __forceinline__ void st16_device(void* base, uint32_t off, uint4_t v) {
+  const auto r = __builtin_amdgcn_make_buffer_rsrc(base, 0, 0x7fffffff, kBufferWord3);
+  __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, kScopeDevice);
+}
+__device__ __forceinline__ uint4_t ld16_device(const void* base, uint32_t off) {
+  const auto r = __builtin_amdgcn_make_buffer_rsrc((void*)base, 0, 0x7fffffff, kBufferWord3);
+  return __builtin_bit_cast(uint4_t, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kScopeDevice));
+}
 
 }  // namespace akt

@@ -16,7 +16,12 @@
 // unit and its four waves take 16-token groups round-robin.  Each wave keeps
 // an online softmax in registers, the waves are merged through LDS, and the
 // workgroup writes either the final output (single-chunk units) or a partial
-// (m, l, o) that split_combine_kernel merges with a log-sum-exp combine.
+// (m, l, o).  The log-sum-exp combine of a unit's partials runs in the same
+// launch: each partial is stored with device-scope (sc1) stores, the
+// workgroup then counts itself in the unit's arrival counter, and the
+// workgroup that arrives last reads every partial back with device-scope
+// loads and writes the unit's output.  No L2 write-back fence is needed (the
+// partials never sit dirty in one XCD's L2) and no second kernel runs.
 //
 // Per 16-token group a wave computes the 16 x GT score block with four (D=128)
 // v_mfma_f32_16x16x32_f16: A = K rows (token = lane & 15, each lane holds a
@@ -40,12 +45,13 @@ constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / kWave;
 // Split-KV chunk lengths (tokens) of dense and paged caches: 128, 256, 512 or
 // 640, i.e. 2, 4, 8 or 10 16-token groups per wave.
-constexpr int kMaxChunk = 640;
 // Largest batch whose paged chunk table fits the persistent kernel's LDS.
 constexpr int kMaxTableB = 1024;
 constexpr int kMaxDevices = 64;
 // Workspace header holding the scheduling counters; zero between launches.
 constexpr size_t kCounterBytes = 256;
+// Partials are addressed with 32-bit byte offsets.
+constexpr int64_t kMaxPartialBytes = (int64_t)1 << 31;
 #define AKT_NEG_INF (-__builtin_inff())
 
 struct SplitParams {
@@ -62,7 +68,8 @@ struct SplitParams {
   const float* lsh_l;
   half_t* o;      // [B, Hq, D] contiguous
   float* lse;     // [B, Hq] or null
-  int* counters;   // [2]: work tickets, exited workgroups (zero between launches)
+  int* counters;  // [2]: work tickets, exited workgroups (zero between launches)
+  int* arrive;    // [units]: partials stored so far per unit (zero between launches)
   float* part_o;  // [parts, GT, D]
   float* part_ml; // [parts, GT, 4]: running max, fp16-P normaliser, fp32 normaliser, pad
   int64_t q_sb, q_sh;
@@ -128,28 +135,6 @@ __device__ bool locate_chunk(const SplitParams& p, int x, int& b_out, int& c_out
   return false;
 }
 
-// Wave-cooperative: first global chunk and chunk count of sequence b.
-__device__ void chunk_span(const SplitParams& p, int b, int& cs_out, int& nch_out) {
-  const int lane = threadIdx.x & 63;
-  int acc = 0, mine = 0;
-  for (int base = 0; base < p.B; base += 64) {
-    const int bb = base + lane;
-    if (bb < p.B && bb <= b) {
-      int len = paged_len(p.indptr, p.last_len, bb, p.page_size);
-      int n = (len + p.chunk - 1) / p.chunk;
-      if (bb < b) acc += n;
-      else mine = n;
-    }
-  }
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) {
-    acc += __shfl_xor(acc, off, 64);
-    mine += __shfl_xor(mine, off, 64);
-  }
-  cs_out = acc;
-  nch_out = mine;
-}
-
 // MagicPIG correction ln u for one token (eq. 11 of the reference's
 // attention_with_norm.png, as evaluated in
 // magicpig_sparsetoken_decode_flash_attention_redundant_var_len_paged_with_norm.py:110-160):
@@ -185,9 +170,12 @@ __device__ __forceinline__ float magicpig_log_u(float cosv, float K, float L) {
 // Split kernel.
 // ---------------------------------------------------------------------------
 // Resolved work item: a chunk [t0, t1) of one unit (wave-uniform values).
+// The unit's chunks c = 0 .. nch - 1 keep their partials at partial index
+// pfirst + c * pstep; pidx is this item's.
 struct Item {
   int b, kvh, hq0, nh, t0, t1, pstart, np, direct;
-  int64_t pidx;
+  int nch, unit, pstep;
+  int64_t pidx, pfirst;
   int64_t ind_off;  // sparse: offset of the unit's kept-index row in sparse_ind
 };
 
@@ -209,8 +197,16 @@ struct IssueCtx {
 // followed by the first two of the next, issued before the item's
 // workgroup merge, so the memory pipeline never drains between items.
 // Otherwise (sparse units) one workgroup handles the item named by blockIdx.
+// Two workgroups per CU (two waves per SIMD) is what hides a unit's load
+// latency; instances whose state fits in 256 registers per lane are held to it.
+template <int D, int GT>
+constexpr int split_min_waves() {
+  return (D <= 128 && GT <= 4) ? 2 : 1;
+}
+
 template <int D, int GT, int MODE, bool ALIGNED, bool MAGIC, int GPW, bool PERSIST>
-__global__ __launch_bounds__(kThreads) void split_kernel(SplitParams p) {
+__global__ __launch_bounds__(kThreads)
+__attribute__((amdgpu_waves_per_eu(split_min_waves<D, GT>(), 8))) void split_kernel(SplitParams p) {
   constexpr int KPL = D / 4;                 // K elements per lane per group
   constexpr int KS = D / 32;                 // MFMA k-steps (8 elements each)
   constexpr int VTOK = (D == 64) ? 2 : 4;    // V tokens per lane per group
@@ -225,10 +221,13 @@ __global__ __launch_bounds__(kThreads) void split_kernel(SplitParams p) {
   static_assert(GPW == 0 || GPW >= 2, "the cross-item pipeline needs two groups per wave");
   constexpr bool TABLE = PERSIST && MODE == kModePaged;
 
-  __shared__ float sm_o[kWaves][GT][D];
+  __shared__ __attribute__((aligned(16))) float sm_o[kWaves][GT][D];
   __shared__ float sm_m[kWaves][GT];
   __shared__ float sm_l[kWaves][GT];
   __shared__ float sm_e[kWaves][GT];
+  __shared__ int sm_last;   // this workgroup stored the unit's last partial
+  __shared__ int sm_pflag;  // ... of the pending item's unit (persistent loop)
+  __shared__ Item sm_pend;  // the pending item (persistent loop; written by thread 0)
   // Paged persistent: chunk prefix, length and first page of every sequence.
   __shared__ int sm_cs[TABLE ? kMaxTableB + 1 : 1];
   __shared__ int sm_len[TABLE ? kMaxTableB : 1];
@@ -254,6 +253,10 @@ __global__ __launch_bounds__(kThreads) void split_kernel(SplitParams p) {
     w.t1 = min(len, w.t0 + p.chunk);
     w.pidx = (int64_t)x * Y + y;
     w.direct = (nch == 1);
+    w.nch = nch;
+    w.unit = w.b * Y + y;
+    w.pfirst = (int64_t)(x - c) * Y + y;  // chunk x - c is the sequence's first
+    w.pstep = Y;
   };
   // Item i of the persistent order: chunk index x = i / Y, unit y = i % Y.
   auto resolve_persistent = [&](int i) -> Item {
@@ -314,6 +317,10 @@ __global__ __launch_bounds__(kThreads) void split_kernel(SplitParams p) {
       w.t1 = max(w.t0, min(n, w.t0 + per));
       w.pidx = x;
       w.direct = (p.n_split == 1);
+      w.nch = p.n_split;
+      w.unit = u;
+      w.pfirst = (int64_t)u * p.n_split;
+      w.pstep = 1;
       if constexpr (MODE == kModeSparsePaged) {
         w.pstart = p.indptr[w.b];
         w.np = p.indptr[w.b + 1] - w.pstart;
@@ -333,6 +340,9 @@ __global__ __launch_bounds__(kThreads) void split_kernel(SplitParams p) {
     w.pstart = uniform(w.pstart);
     w.np = uniform(w.np);
     w.direct = uniform(w.direct);
+    w.nch = uniform(w.nch);
+    w.unit = uniform(w.unit);
+    w.pstep = uniform(w.pstep);
   };
 
   // ---- per-item setup: issue context (with page prefetch) and q fragment ----
@@ -594,8 +604,135 @@ __global__ __launch_bounds__(kThreads) void split_kernel(SplitParams p) {
     }
   };
 
-  // Wave reduction, workgroup merge and output of the current item.
-  auto finish = [&]() {
+  // ---- output of a unit ----------------------------------------------------
+  constexpr int NV = GT * D / 4;  // float4 vectors of a unit's output (head-major)
+  // Arrival of a stored partial is counted one item late in the persistent
+  // loop (see the driver), which needs the item's third group.
+  constexpr bool DEFER = PERSIST && GPW >= 3;
+  // Normalised output of head h of item w, dims d0 .. d0 + 3, and (d0 == 0) its LSE.
+  auto write_out = [&](const Item& w, int h, int d0, float4_t O, float M, float L, float E) {
+    const int64_t row = (int64_t)w.b * p.Hq + w.hq0 + h;
+    const float inv = L > 0.f ? 1.0f / L : 0.f;
+    half4_t hv;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) hv[r] = (half_t)(O[r] * inv);
+    *reinterpret_cast<half4_t*>(p.o + row * D + d0) = hv;
+    if (d0 == 0 && p.lse) p.lse[row] = E > 0.f ? (M + log2f(E)) * kLn2 : AKT_NEG_INF;
+  };
+
+  // Log-sum-exp merge of the nch partials of item w's unit, run by the
+  // workgroup that counted the last of them.  A thread owns one float4 of one
+  // head's output and walks its chunk group's chunks c = cg, cg + NG, ...
+  // with an online max, U chunks per round trip of device-scope loads; the
+  // chunk groups are then merged through LDS.  Called by every thread after a
+  // barrier that follows the last read of the merge buffers.
+  auto merge_unit = [&](const Item& w) {
+    constexpr int NG = NV >= kThreads ? 1 : (kThreads / NV < kWaves ? kThreads / NV : kWaves);
+    constexpr int U = 8;
+    const int nch = w.nch;
+    auto combine = [](float& M, float& L, float& E, float4_t& A, float m, float l, float e,
+                      float4_t a) {
+      if (m == AKT_NEG_INF) return;
+      if (m > M) {
+        const float s = fast_exp2(M - m);  // 0 while M = -inf (A, L, E are 0 then)
+        A *= s;
+        L *= s;
+        E *= s;
+        M = m;
+      }
+      const float f = fast_exp2(m - M);
+      A += f * a;
+      L += f * l;
+      E += f * e;
+    };
+    auto accumulate = [&](int vec, int cg, float& M, float& L, float& E, float4_t& A) {
+      const int h = (vec * 4) / D;
+      const int d0 = vec * 4 - h * D;
+      M = AKT_NEG_INF;
+      L = E = 0.f;
+      A = float4_t{0.f, 0.f, 0.f, 0.f};
+      for (int c0 = cg; c0 < nch; c0 += U * NG) {
+        float4_t ml[U], ov[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int c = min(c0 + u * NG, nch - 1);
+          const int64_t ph = (w.pfirst + (int64_t)c * w.pstep) * GT + h;
+          ml[u] = as_float4u(ld16_device(p.part_ml, (uint32_t)(ph * 16)));
+          ov[u] = as_float4u(ld16_device(p.part_o, (uint32_t)((ph * D + d0) * 4)));
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+          if (c0 + u * NG < nch) combine(M, L, E, A, ml[u][0], ml[u][1], ml[u][2], ov[u]);
+      }
+    };
+    if constexpr (NG == 1) {
+      for (int vec = tid; vec < NV; vec += kThreads) {
+        float M, L, E;
+        float4_t A;
+        accumulate(vec, 0, M, L, E, A);
+        const int h = (vec * 4) / D;
+        if (h < w.nh) write_out(w, h, vec * 4 - h * D, A, M, L, E);
+      }
+    } else {
+      const int vec = tid % NV;
+      const int cg = tid / NV;
+      const int h = (vec * 4) / D;
+      const int d0 = vec * 4 - h * D;
+      float M = AKT_NEG_INF, L = 0.f, E = 0.f;
+      float4_t A = {0.f, 0.f, 0.f, 0.f};
+      if (cg < NG) accumulate(vec, cg, M, L, E, A);
+      float4_t* red = reinterpret_cast<float4_t*>(&sm_o[0][0][0]);  // [NG - 1][NV]
+      if (cg >= 1 && cg < NG) {
+        red[(cg - 1) * NV + vec] = A;
+        if (d0 == 0) {
+          sm_m[cg][h] = M;
+          sm_l[cg][h] = L;
+          sm_e[cg][h] = E;
+        }
+      }
+      __syncthreads();
+      if (cg == 0) {
+#pragma unroll
+        for (int g2 = 1; g2 < NG; ++g2)
+          combine(M, L, E, A, sm_m[g2][h], sm_l[g2][h], sm_e[g2][h], red[(g2 - 1) * NV + vec]);
+        if (h < w.nh) write_out(w, h, d0, A, M, L, E);
+      }
+    }
+  };
+
+  // Counts item w's stored partial in its unit's arrival counter (thread 0)
+  // and returns, to every thread, whether this workgroup stored the unit's
+  // last partial; the last one also resets the counter for the next launch.
+  // Every thread first waits for its outstanding memory operations, so wave
+  // 0's partial stores are complete (visible device-wide) before the count.
+  auto arrive_now = [&](const Item& w) -> bool {
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (tid == 0) {
+      const int prev = atomicAdd(&p.arrive[w.unit], 1);
+      const int last = prev == w.nch - 1;
+      if (last) atomicExch(&p.arrive[w.unit], 0);
+      sm_last = last;
+    }
+    __syncthreads();
+    return sm_last != 0;
+  };
+
+  // Persistent (DEFER) arrival state: sm_pend is the item whose partial was
+  // stored at the previous finish() and is counted by thread 0 during the
+  // current item (arr holds the counter's old value).  It lives in LDS: only
+  // thread 0 and the rare merge read it, and registers are the scarce resource.
+  bool has_pend = false;
+  int arr = -1;
+
+  // Wave reduction, workgroup merge and output of the current item; returns
+  // the ticket thread 0 published in sm_next before the call.  A multi-chunk
+  // item's partial is stored by wave 0 alone (so one wave's memory ordering
+  // covers all of it) with device-scope stores.  Without DEFER the workgroup
+  // then counts it at once and merges the unit if it was last.  With DEFER it
+  // becomes sm_pend, and the previous pending item, counted during this item,
+  // is merged here if this workgroup stored its unit's last partial (sm_pflag).
+  auto finish = [&]() -> int {
     const float l_wave = rows_sum(l_part);
     const float e_wave = rows_sum(e_part);
 #pragma unroll
@@ -622,41 +759,76 @@ __global__ __launch_bounds__(kThreads) void split_kernel(SplitParams p) {
       }
     }
     __syncthreads();
-    const int b = it.b, hq0 = it.hq0, nh = it.nh;
-    const int64_t pidx = it.pidx;
-    for (int idx = tid; idx < GT * D; idx += kThreads) {
-      const int h = idx / D;
-      const int d = idx - h * D;
-      float M = AKT_NEG_INF;
+    // Thread 0 wrote the next ticket (and the pending item's count) before
+    // the barrier above; every wave reads them before the last barrier below,
+    // so thread 0 cannot overwrite them while a wave still has to read them.
+    const int next_ticket = sm_next;
+    const bool merge_pend = DEFER && has_pend && sm_pflag != 0;
+    const float4_t* sm_o4 = reinterpret_cast<const float4_t*>(&sm_o[0][0][0]);
+    auto wave_merge = [&](int vec, float& M, float& L, float& E, float4_t& O) {
+      const int h = (vec * 4) / D;
+      M = AKT_NEG_INF;
 #pragma unroll
       for (int w = 0; w < kWaves; ++w) M = fmaxf(M, sm_m[w][h]);
-      float L = 0.f, E = 0.f, O = 0.f;
+      L = E = 0.f;
+      O = float4_t{0.f, 0.f, 0.f, 0.f};
       if (M != AKT_NEG_INF) {
 #pragma unroll
         for (int w = 0; w < kWaves; ++w) {
           const float f = fast_exp2(sm_m[w][h] - M);
           L += f * sm_l[w][h];
           E += f * sm_e[w][h];
-          O += f * sm_o[w][h][d];
+          O += f * sm_o4[w * NV + vec];
         }
       }
-      if (h >= nh) continue;
-      if (it.direct) {
-        const int64_t row = (int64_t)b * p.Hq + hq0 + h;
-        p.o[row * D + d] = (half_t)(L > 0.f ? O / L : 0.f);
-        if (d == 0 && p.lse) p.lse[row] = E > 0.f ? (M + log2f(E)) * kLn2 : AKT_NEG_INF;
-      } else {
-        p.part_o[(pidx * GT + h) * D + d] = O;
-        if (d == 0) {
-          float* ml = p.part_ml + (pidx * GT + h) * 4;
-          ml[0] = M;
-          ml[1] = L;
-          ml[2] = E;
-          ml[3] = 0.f;
-        }
+    };
+    if (it.direct) {
+      for (int vec = tid; vec < NV; vec += kThreads) {
+        const int h = (vec * 4) / D;
+        if (h >= it.nh) continue;
+        float M, L, E;
+        float4_t O;
+        wave_merge(vec, M, L, E, O);
+        write_out(it, h, vec * 4 - h * D, O, M, L, E);
+      }
+    } else if (wave == 0) {
+      for (int vec = lane; vec < NV; vec += kWave) {
+        const int h = (vec * 4) / D;
+        if (h >= it.nh) continue;
+        float M, L, E;
+        float4_t O;
+        wave_merge(vec, M, L, E, O);
+        const int64_t ph = it.pidx * GT + h;
+        st16_device(p.part_o, (uint32_t)((ph * D + vec * 4 - h * D) * 4), as_uint4f(O));
+        if (vec * 4 == h * D)
+          st16_device(p.part_ml, (uint32_t)(ph * 16), as_uint4f(float4_t{M, L, E, 0.f}));
       }
     }
+    if constexpr (DEFER) {
+      if (merge_pend) {  // workgroup-uniform
+        if (tid == 0) atomicExch(&p.arrive[sm_pend.unit], 0);
+        __syncthreads();  // the merge buffers are read above
+        merge_unit(sm_pend);
+      }
+    } else {
+      if (!it.direct && arrive_now(it)) merge_unit(it);  // workgroup-uniform
+    }
     __syncthreads();  // the merge buffers are reused by the next item
+    if constexpr (DEFER) {
+      // Every read of the previous sm_pend is above the barrier; thread 0
+      // itself reads the new one next, the other threads after later barriers.
+      has_pend = !it.direct;
+      if (has_pend && tid == 0) sm_pend = it;
+    }
+    return next_ticket;
+  };
+
+  // Sequence bb has no tokens: o = 0 and lse = -inf for all its query heads.
+  auto zero_sequence = [&](int bb) {
+    half_t* orow = p.o + (int64_t)bb * p.Hq * D;
+    for (int i = tid; i < p.Hq * (D / 8); i += kThreads) st16(orow + 8 * i, uint4_t{0, 0, 0, 0});
+    if (p.lse)
+      for (int h = tid; h < p.Hq; h += kThreads) p.lse[(int64_t)bb * p.Hq + h] = AKT_NEG_INF;
   };
 
   // ---- drivers ---------------------------------------------------------------
@@ -698,6 +870,9 @@ __global__ __launch_bounds__(kThreads) void split_kernel(SplitParams p) {
       if (tid == 0) sm_cs[p.B] = carry;
       __syncthreads();
       n_items = sm_cs[p.B] * Y;
+      // Sequences without tokens have no items: their rows are written here.
+      for (int bb = blockIdx.x; bb < p.B; bb += gridDim.x)
+        if (sm_len[bb] == 0) zero_sequence(bb);
     } else {
       n_items = p.B * ((p.S + p.chunk - 1) / p.chunk) * Y;
     }
@@ -718,7 +893,7 @@ __global__ __launch_bounds__(kThreads) void split_kernel(SplitParams p) {
     // exit resets both counters to zero for the next launch.
     int i = blockIdx.x;
     int nxt = i + (int)gridDim.x;
-    int pending = 0;
+    int ticket_raw = 0;  // thread 0: counters[0] before its increment
     if (i < n_items) {  // workgroup-uniform; the grid is sized from an upper bound
     Item nx;
     IssueCtx cc, nc;
@@ -733,20 +908,37 @@ __global__ __launch_bounds__(kThreads) void split_kernel(SplitParams p) {
     issue(cc, cc.g_begin + wave, bufs[0]);
     issue(cc, cc.g_begin + wave + kWaves, bufs[1]);
     for (;;) {
-      if (tid == 0) pending = 2 * (int)gridDim.x + atomicAdd(&p.counters[0], 1);
+      // The returned value is first used at the item's end (adding the offset
+      // here would make the wave wait for the loads in flight at once).
+      if (tid == 0) ticket_raw = atomicAdd(&p.counters[0], 1);
       begin_item();
       // Groups k of this item; the prefetch two groups ahead crosses into the
       // next item for the last two (k + 2 >= GPW is a compile-time condition).
 #pragma unroll
       for (int k = 0; k < GPW; ++k) {
         consume(bufs[k & 1]);
+        if constexpr (DEFER) {
+          if (k == 2 && has_pend && tid == 0) {
+            // Group 2's loads were issued after the pending partial's stores
+            // (at the previous finish()), and wave 0 has just waited for
+            // them: in-order completion makes those stores complete too.
+            // The empty asm consumes a word of group 2 and yields 0, so the
+            // count cannot be issued before that wait.
+            int zero = 0;
+            asm volatile("" : "+s"(zero) : "v"(bufs[0].k[0][0]));
+            arr = atomicAdd(&p.arrive[sm_pend.unit + zero], 1);
+          }
+        }
         if (k + 2 < GPW) issue(cc, cc.g_begin + wave + kWaves * (k + 2), bufs[k & 1]);
         else issue(nc, nc.g_begin + wave + kWaves * (k + 2 - GPW), bufs[k & 1]);
       }
-      if (tid == 0) sm_next = pending;  // published by finish()'s first barrier
-      finish();
+      if (tid == 0) {  // read back by finish() after its first barrier
+        sm_next = 2 * (int)gridDim.x + ticket_raw;
+        if constexpr (DEFER) sm_pflag = has_pend && arr == sm_pend.nch - 1;
+      }
+      const int ticket = finish();
       const int inext = nxt;
-      nxt = sm_next;
+      nxt = ticket;
       if (inext >= n_items) break;  // the last prefetch read q rows (see resolve_next)
       i = inext;
       it = nx;
@@ -758,6 +950,10 @@ __global__ __launch_bounds__(kThreads) void split_kernel(SplitParams p) {
       setup(nx, nc, qn);
     }
     }  // i < n_items
+    if constexpr (DEFER) {
+      // The last item's partial has not been counted yet.
+      if (has_pend && arrive_now(sm_pend)) merge_unit(sm_pend);  // workgroup-uniform
+    }
     if (tid == 0) {
       if (atomicAdd(&p.counters[1], 1) == (int)gridDim.x - 1) {
         atomicExch(&p.counters[0], 0);
@@ -765,6 +961,12 @@ __global__ __launch_bounds__(kThreads) void split_kernel(SplitParams p) {
       }
     }
   } else {
+    if constexpr (MODE == kModePaged) {
+      // Sequences without tokens have no chunk (grid.x >= B).
+      if (blockIdx.y == 0 && (int)blockIdx.x < p.B &&
+          paged_len(p.indptr, p.last_len, blockIdx.x, p.page_size) == 0)
+        zero_sequence(blockIdx.x);
+    }
     it = resolve_block();
     if (it.b < 0) return;  // workgroup-uniform
     make_uniform(it);
@@ -808,144 +1010,13 @@ __global__ __launch_bounds__(kThreads) void split_kernel(SplitParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// Log-sum-exp combine of split partials.
+// Rows of an empty dense cache: o = 0, lse = -inf.
 // ---------------------------------------------------------------------------
-template <int D, int GT, int MODE>
-__global__ __launch_bounds__(kThreads) void split_combine_kernel(SplitParams p) {
-  // One workgroup merges the partials of one unit (GT heads x D dims) in one
-  // global round trip for up to 8 * NG chunks: every thread first issues its
-  // partial-output loads and the workgroup copies the chunks' (m, l, e) rows
-  // to LDS; after one barrier each thread derives its head's max and
-  // normalisers from LDS and accumulates.  Only the final chunk-group
-  // reduction goes through LDS again.
-  constexpr bool SPARSE = (MODE == kModeSparseDense || MODE == kModeSparsePaged);
-  constexpr int NV = GT * D / 4;                          // float4 output vectors
-  constexpr int NG = NV >= kThreads ? 1 : kThreads / NV;  // chunk groups
-  constexpr int MLCAP = 1024 / GT;                        // chunk rows kept in LDS
-  __shared__ float4_t sm_ml[MLCAP * GT];
-  __shared__ float4_t sm_o[NG > 1 ? kThreads : 1];
-
-  const int tid = threadIdx.x;
-  int b, hq0, nh, nch;
-  int64_t first, step;
-  if constexpr (SPARSE) {
-    const int u = blockIdx.x;
-    b = u / p.Hq;
-    hq0 = u - b * p.Hq;
-    nh = 1;
-    nch = p.n_split;
-    first = (int64_t)u * p.n_split;
-    step = 1;
-  } else {
-    b = blockIdx.x;
-    const int y = blockIdx.y;
-    const int kvh = y / p.n_hg;
-    const int hg = y - kvh * p.n_hg;
-    hq0 = kvh * p.G + hg * GT;
-    nh = min(GT, p.G - hg * GT);
-    int cs;
-    if constexpr (MODE == kModeDense) {
-      nch = (p.S + p.chunk - 1) / p.chunk;
-      cs = b * nch;
-    } else {
-      chunk_span(p, b, cs, nch);
-    }
-    first = (int64_t)cs * gridDim.y + y;
-    step = gridDim.y;
-  }
-  if (nch == 1) return;  // the split kernel wrote this unit's output directly
-  if (nch == 0) {        // empty unit: no partials exist
-    for (int idx = tid; idx < nh * D; idx += kThreads) {
-      const int h = idx / D;
-      const int64_t row = (int64_t)b * p.Hq + hq0 + h;
-      p.o[row * D + (idx - h * D)] = (half_t)0.f;
-      if (idx - h * D == 0 && p.lse) p.lse[row] = AKT_NEG_INF;
-    }
-    return;
-  }
-  auto ml = [&](int c, int h) -> float4_t {
-    return *reinterpret_cast<const float4_t*>(p.part_ml + ((first + c * step) * GT + h) * 4);
-  };
-  auto po = [&](int c, int h, int d0) -> float4_t {
-    return *reinterpret_cast<const float4_t*>(p.part_o + ((first + c * step) * GT + h) * D + d0);
-  };
-
-  // Round trip: partial outputs of the first U chunks of this thread's chunk
-  // group, and the (m, l, e) rows of up to MLCAP chunks into LDS.
-  constexpr int U = 8;
-  constexpr int VSTEP = kThreads / NG;  // output vectors per pass
-  constexpr int NPASS = (NV + VSTEP - 1) / VSTEP;
-  const int cg = tid / VSTEP;
-  float4_t ov[NPASS][U];
-#pragma unroll
-  for (int ps = 0; ps < NPASS; ++ps) {
-    const int vec = min(ps * VSTEP + tid % VSTEP, NV - 1);
-    const int h = (vec * 4) / D;
-    const int d0 = vec * 4 - h * D;
-#pragma unroll
-    for (int u = 0; u < U; ++u) ov[ps][u] = po(max(0, min(cg + u * NG, nch - 1)), h, d0);
-  }
-  const int nml = min(nch, MLCAP);
-  for (int i = tid; i < nml * GT; i += kThreads) sm_ml[i] = ml(i / GT, i % GT);
-  __syncthreads();
-  auto mlrow = [&](int c, int h) -> float4_t { return c < MLCAP ? sm_ml[c * GT + h] : ml(c, h); };
-
-#pragma unroll
-  for (int ps = 0; ps < NPASS; ++ps) {
-    const int vec = ps * VSTEP + tid % VSTEP;
-    const int h = (min(vec, NV - 1) * 4) / D;
-    const int d0 = min(vec, NV - 1) * 4 - h * D;
-    // Head h's max and the two normalisers (every thread of the head computes
-    // the same values from broadcast LDS reads).
-    float M = AKT_NEG_INF;
-    for (int c = 0; c < nch; ++c) M = fmaxf(M, mlrow(c, h)[0]);
-    float L = 0.f, E = 0.f;
-    if (M != AKT_NEG_INF) {
-      for (int c = 0; c < nch; ++c) {
-        const float4_t v = mlrow(c, h);
-        const float w = fast_exp2(v[0] - M);
-        L += w * v[1];
-        E += w * v[2];
-      }
-    }
-    auto weight = [&](int c) -> float {
-      return M == AKT_NEG_INF ? 0.f : fast_exp2(mlrow(c, h)[0] - M);
-    };
-    float4_t acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int c = cg + u * NG;
-      if (c < nch) acc += weight(c) * ov[ps][u];
-    }
-    // Remaining chunks in batches of U independent loads (one round trip each).
-    for (int c0 = cg + U * NG; c0 < nch; c0 += U * NG) {
-      float4_t ob[U];
-#pragma unroll
-      for (int u = 0; u < U; ++u) ob[u] = po(min(c0 + u * NG, nch - 1), h, d0);
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int c = c0 + u * NG;
-        if (c < nch) acc += weight(c) * ob[u];
-      }
-    }
-    if constexpr (NG > 1) {
-      sm_o[tid] = acc;
-      __syncthreads();
-      if (cg == 0) {
-        for (int i = 1; i < NG; ++i) acc += sm_o[tid + i * VSTEP];
-      }
-      __syncthreads();
-    }
-    if (cg == 0 && vec < NV && h < nh) {
-      const float inv = L > 0.f ? 1.0f / L : 0.f;
-      const int64_t row = (int64_t)b * p.Hq + hq0 + h;
-      half4_t hv;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) hv[r] = (half_t)(acc[r] * inv);
-      *reinterpret_cast<half4_t*>(p.o + row * D + d0) = hv;
-      if (d0 == 0 && p.lse) p.lse[row] = E > 0.f ? (M + log2f(E)) * kLn2 : AKT_NEG_INF;
-    }
-  }
+__global__ __launch_bounds__(kThreads) void empty_rows_kernel(half_t* o, float* lse, int64_t rows,
+                                                              int D) {
+  const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (i < rows * (D / 8)) st16(o + 8 * i, uint4_t{0, 0, 0, 0});
+  if (lse && i < rows) lse[i] = AKT_NEG_INF;
 }
 
 // ---------------------------------------------------------------------------
@@ -996,50 +1067,38 @@ int launch_split(const SplitParams& p, dim3 grid, hipStream_t st) {
 }
 
 template <int D, int GT, int MODE, bool ALIGNED, bool MAGIC>
-int launch_t(const SplitParams& p, dim3 grid, dim3 cgrid, hipStream_t st) {
+int launch_t(const SplitParams& p, dim3 grid, hipStream_t st) {
   constexpr bool SPARSE = (MODE == kModeSparseDense || MODE == kModeSparsePaged);
-  int rc = AKT_OK;
-  if (grid.x > 0 && grid.y > 0) {
-    if constexpr (SPARSE) {
-      rc = launch_split<D, GT, MODE, ALIGNED, MAGIC, 0, false>(p, grid, st);
-    } else if constexpr (MODE == kModePaged && !ALIGNED) {
-      // Pages that do not hold whole 16-token groups: 256-token chunks only.
-      if (p.B <= kMaxTableB) rc = launch_split<D, GT, MODE, false, MAGIC, 4, true>(p, grid, st);
-      else rc = launch_split<D, GT, MODE, false, MAGIC, 4, false>(p, grid, st);
-    } else {
-      // A chunk of `chunk` tokens is chunk / 64 16-token groups per wave.
-      bool persist = true;
-      if constexpr (MODE == kModePaged) persist = p.B <= kMaxTableB;
-      if constexpr (MODE == kModePaged) {
-        if (!persist) rc = launch_split<D, GT, MODE, ALIGNED, MAGIC, 4, false>(p, grid, st);
-      }
-      if (!persist) {
-      } else if (p.chunk == 128) rc = launch_split<D, GT, MODE, ALIGNED, MAGIC, 2, true>(p, grid, st);
-      else if (p.chunk == 256) rc = launch_split<D, GT, MODE, ALIGNED, MAGIC, 4, true>(p, grid, st);
-      else if (p.chunk == 640) rc = launch_split<D, GT, MODE, ALIGNED, MAGIC, 10, true>(p, grid, st);
-      else rc = launch_split<D, GT, MODE, ALIGNED, MAGIC, 8, true>(p, grid, st);
+  if constexpr (SPARSE) {
+    return launch_split<D, GT, MODE, ALIGNED, MAGIC, 0, false>(p, grid, st);
+  } else if constexpr (MODE == kModePaged && !ALIGNED) {
+    // Pages that do not hold whole 16-token groups: 256-token chunks only.
+    if (p.B <= kMaxTableB) return launch_split<D, GT, MODE, false, MAGIC, 4, true>(p, grid, st);
+    return launch_split<D, GT, MODE, false, MAGIC, 4, false>(p, grid, st);
+  } else {
+    // A chunk of `chunk` tokens is chunk / 64 16-token groups per wave.
+    if constexpr (MODE == kModePaged) {
+      if (p.B > kMaxTableB) return launch_split<D, GT, MODE, ALIGNED, MAGIC, 4, false>(p, grid, st);
     }
-    if (rc) return rc;
+    if (p.chunk == 128) return launch_split<D, GT, MODE, ALIGNED, MAGIC, 2, true>(p, grid, st);
+    if (p.chunk == 256) return launch_split<D, GT, MODE, ALIGNED, MAGIC, 4, true>(p, grid, st);
+    if (p.chunk == 640) return launch_split<D, GT, MODE, ALIGNED, MAGIC, 10, true>(p, grid, st);
+    return launch_split<D, GT, MODE, ALIGNED, MAGIC, 8, true>(p, grid, st);
   }
-  if (cgrid.x > 0 && cgrid.y > 0) {
-    hipLaunchKernelGGL((split_combine_kernel<D, GT, MODE>), cgrid, dim3(kThreads), 0, st, p);
-    rc = check_launch("split_combine_kernel");
-  }
-  return rc;
 }
 
 template <int D, int MODE, bool ALIGNED, bool MAGIC>
-int launch_gt(int gt, const SplitParams& p, dim3 grid, dim3 cgrid, hipStream_t st) {
+int launch_gt(int gt, const SplitParams& p, dim3 grid, hipStream_t st) {
   if constexpr (MODE == kModeSparseDense || MODE == kModeSparsePaged) {
-    return launch_t<D, 1, MODE, ALIGNED, MAGIC>(p, grid, cgrid, st);
+    return launch_t<D, 1, MODE, ALIGNED, MAGIC>(p, grid, st);
   } else {
     switch (gt) {
-      case 1: return launch_t<D, 1, MODE, ALIGNED, MAGIC>(p, grid, cgrid, st);
-      case 2: return launch_t<D, 2, MODE, ALIGNED, MAGIC>(p, grid, cgrid, st);
-      case 4: return launch_t<D, 4, MODE, ALIGNED, MAGIC>(p, grid, cgrid, st);
-      case 8: return launch_t<D, 8, MODE, ALIGNED, MAGIC>(p, grid, cgrid, st);
+      case 1: return launch_t<D, 1, MODE, ALIGNED, MAGIC>(p, grid, st);
+      case 2: return launch_t<D, 2, MODE, ALIGNED, MAGIC>(p, grid, st);
+      case 4: return launch_t<D, 4, MODE, ALIGNED, MAGIC>(p, grid, st);
+      case 8: return launch_t<D, 8, MODE, ALIGNED, MAGIC>(p, grid, st);
       case 16:
-        if constexpr (D != 256) return launch_t<D, 16, MODE, ALIGNED, MAGIC>(p, grid, cgrid, st);
+        if constexpr (D != 256) return launch_t<D, 16, MODE, ALIGNED, MAGIC>(p, grid, st);
         break;
     }
     return set_error(AKT_ERR_UNSUPPORTED, "no decode kernel for %d heads per unit", gt);
@@ -1047,13 +1106,80 @@ int launch_gt(int gt, const SplitParams& p, dim3 grid, dim3 cgrid, hipStream_t s
 }
 
 template <int MODE, bool ALIGNED, bool MAGIC>
-int launch_d(int D, int gt, const SplitParams& p, dim3 grid, dim3 cgrid, hipStream_t st) {
+int launch_d(int D, int gt, const SplitParams& p, dim3 grid, hipStream_t st) {
   switch (D) {
-    case 64: return launch_gt<64, MODE, ALIGNED, MAGIC>(gt, p, grid, cgrid, st);
-    case 128: return launch_gt<128, MODE, ALIGNED, MAGIC>(gt, p, grid, cgrid, st);
-    case 256: return launch_gt<256, MODE, ALIGNED, MAGIC>(gt, p, grid, cgrid, st);
+    case 64: return launch_gt<64, MODE, ALIGNED, MAGIC>(gt, p, grid, st);
+    case 128: return launch_gt<128, MODE, ALIGNED, MAGIC>(gt, p, grid, st);
+    case 256: return launch_gt<256, MODE, ALIGNED, MAGIC>(gt, p, grid, st);
   }
   return set_error(AKT_ERR_UNSUPPORTED, "head_dim %d not supported (64, 128, 256)", D);
+}
+
+// Workspace layout of a split launch: the counter header, the arrival
+// counters, then the partial outputs [parts, GT, D] and their (m, l, e, pad)
+// rows [parts, GT, 4], all fp32.  Arrival counters must be zero when a launch
+// starts and every launch leaves its own at zero, but a workspace is shared by
+// calls of different shapes, so partials of one call must never land where
+// another call looks for counters: the first kArriveSlots counters sit in a
+// fixed area that partials never use, and a call with more units than that
+// also zero-fills its extra counters (which may hold an earlier call's
+// partials) before the split kernel runs.  Launches without partials (every
+// unit a single chunk) need no counters.  Partials are addressed with 32-bit
+// byte offsets, so each array must stay below 2 GiB.
+constexpr int64_t kArriveSlots = 32768;
+
+struct WsLayout {
+  size_t arrive, extra_bytes, part_o, part_ml, total;
+  bool fits;
+};
+
+WsLayout ws_layout(int64_t units, int64_t parts, int gt, int64_t D) {
+  WsLayout w = {};
+  w.fits = true;
+  w.arrive = kCounterBytes;
+  if (parts == 0) {
+    w.part_o = w.part_ml = w.total = kCounterBytes;
+    return w;
+  }
+  const int64_t slots = units > kArriveSlots ? units : kArriveSlots;
+  const int64_t po = parts * gt * D * 4, pml = parts * gt * 16;
+  w.extra_bytes = (size_t)(slots - kArriveSlots) * 4;
+  w.part_o = w.arrive + (size_t)round_up(slots * 4, 256);
+  w.part_ml = w.part_o + (size_t)round_up(po, 256);
+  w.total = w.part_ml + (size_t)pml;
+  w.fits = po < kMaxPartialBytes && pml < kMaxPartialBytes;
+  return w;
+}
+
+// Points the kernel's counters and partials into `ws`.
+void bind_workspace(SplitParams& p, void* ws, const WsLayout& w) {
+  char* c = (char*)ws;
+  p.counters = (int*)c;
+  p.arrive = (int*)(c + w.arrive);
+  p.part_o = (float*)(c + w.part_o);
+  p.part_ml = (float*)(c + w.part_ml);
+}
+
+__global__ __launch_bounds__(kThreads) void zero_words_kernel(int* p, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (i < n) p[i] = 0;
+}
+
+// Zero-fills the arrival counters past the fixed area (see ws_layout).
+int clear_extra_arrivals(const SplitParams& p, const WsLayout& w, hipStream_t st) {
+  if (w.extra_bytes == 0) return AKT_OK;
+  const int64_t n = (int64_t)(w.extra_bytes / 4);
+  hipLaunchKernelGGL(zero_words_kernel, dim3((unsigned)ceil_div(n, kThreads)), dim3(kThreads), 0,
+                     st, p.arrive + kArriveSlots, n);
+  return check_launch("zero_words_kernel");
+}
+
+int check_workspace(const WsLayout& w, const void* ws, size_t ws_bytes) {
+  if (!w.fits)
+    return set_error(AKT_ERR_UNSUPPORTED, "split-KV partials exceed 2 GiB; use longer chunks");
+  if (!ws || ws_bytes < w.total)
+    return set_error(AKT_ERR_WORKSPACE, "workspace of %zu bytes required", w.total);
+  return AKT_OK;
 }
 
 // Workgroups of the decode kernels resident at once on MI355X: two per CU
@@ -1104,10 +1230,6 @@ int64_t auto_splits(int64_t rows, int64_t l_max) {
   return s < 1 ? 1 : s;
 }
 
-size_t split_ws_bytes(int64_t parts, int gt, int64_t D) {
-  return (size_t)parts * gt * (D + 4) * sizeof(float);
-}
-
 bool head_dim_ok(int64_t D) { return D == 64 || D == 128 || D == 256; }
 
 int check_common(int64_t B, int64_t Hq, int64_t Hkv, int64_t D) {
@@ -1131,11 +1253,10 @@ extern "C" size_t akt_decode_workspace_size(int64_t batch, int64_t num_q_heads,
   if (batch <= 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads || !head_dim_ok(head_dim)) return 0;
   const int G = (int)(num_q_heads / num_kv_heads);
   const int gt = pick_gt(G, (int)head_dim);
-  const int64_t n_hg = ceil_div(G, gt);
-  const int64_t units = batch * num_kv_heads * n_hg;
-  const int64_t chunk = chunk_tokens > 0 ? chunk_tokens : auto_chunk(seq_len * batch, num_kv_heads * n_hg);
+  const int64_t Y = num_kv_heads * ceil_div(G, gt);
+  const int64_t chunk = chunk_tokens > 0 ? chunk_tokens : auto_chunk(seq_len * batch, Y);
   const int64_t nch = ceil_div(seq_len, chunk);
-  return kCounterBytes + (nch > 1 ? split_ws_bytes(units * nch, gt, head_dim) : 0);
+  return ws_layout(batch * Y, nch > 1 ? batch * Y * nch : 0, gt, head_dim).total;
 }
 
 extern "C" int akt_decode_fwd(const void* q, const void* k, const void* v, void* o, float* lse,
@@ -1158,13 +1279,19 @@ extern "C" int akt_decode_fwd(const void* q, const void* k, const void* v, void*
   const int G = (int)(num_q_heads / num_kv_heads);
   const int gt = pick_gt(G, D);
   const int n_hg = (int)ceil_div(G, gt);
-  const int64_t chunk = chunk_tokens > 0 ? chunk_tokens
-                                         : auto_chunk(seq_len * batch, num_kv_heads * n_hg);
-  const int64_t nch = ceil_div(seq_len, chunk);
   const int64_t Y = num_kv_heads * n_hg;
-  const size_t need = kCounterBytes + (nch > 1 ? split_ws_bytes(batch * Y * nch, gt, D) : 0);
-  if (!workspace || workspace_bytes < need)
-    return set_error(AKT_ERR_WORKSPACE, "workspace of %zu bytes required", need);
+  const int64_t chunk = chunk_tokens > 0 ? chunk_tokens : auto_chunk(seq_len * batch, Y);
+  const int64_t nch = ceil_div(seq_len, chunk);
+  const WsLayout wl = ws_layout(batch * Y, nch > 1 ? batch * Y * nch : 0, gt, D);
+  rc = check_workspace(wl, workspace, workspace_bytes);
+  if (rc) return rc;
+  hipStream_t st = (hipStream_t)stream;
+  if (nch == 0) {  // empty cache: every row is o = 0, lse = -inf
+    const int64_t rows = batch * num_q_heads;
+    hipLaunchKernelGGL(empty_rows_kernel, dim3((unsigned)ceil_div(rows * (D / 8), kThreads)),
+                       dim3(kThreads), 0, st, (half_t*)o, lse, rows, D);
+    return check_launch("empty_rows_kernel");
+  }
 
   SplitParams p = {};
   p.q = (const half_t*)q;
@@ -1172,9 +1299,7 @@ extern "C" int akt_decode_fwd(const void* q, const void* k, const void* v, void*
   p.vbase = (const half_t*)v;
   p.o = (half_t*)o;
   p.lse = lse;
-  p.counters = (int*)workspace;
-  p.part_o = (float*)((char*)workspace + kCounterBytes);
-  p.part_ml = p.part_o + (nch > 1 ? (size_t)batch * Y * nch * gt * D : 0);
+  bind_workspace(p, workspace, wl);
   p.q_sb = q_stride[0];
   p.q_sh = q_stride[1];
   p.k_sa = k_stride[2]; p.k_sb = 0; p.k_batch = k_stride[0]; p.k_head = k_stride[1];
@@ -1184,16 +1309,19 @@ extern "C" int akt_decode_fwd(const void* q, const void* k, const void* v, void*
   p.n_hg = n_hg;
   p.chunk = (int)chunk;
   p.qk_scale = softmax_scale * kLog2e;
-  hipStream_t st = (hipStream_t)stream;
-  // nch == 0 (empty cache): only the combine pass runs and writes 0 / -inf.
-  dim3 grid((unsigned)(batch * nch), (unsigned)Y);
-  dim3 cgrid(nch == 1 ? 0u : (unsigned)batch, (unsigned)Y);
-  return launch_d<kModeDense, false, false>(D, gt, p, grid, cgrid, st);
+  rc = clear_extra_arrivals(p, wl, st);
+  if (rc) return rc;
+  return launch_d<kModeDense, false, false>(D, gt, p, dim3((unsigned)(batch * nch), (unsigned)Y), st);
 }
 
 // ----------------------------- paged decode --------------------------------
 static int64_t paged_grid_x(int64_t total_pages, int64_t page_size, int64_t chunk, int64_t batch) {
   return ceil_div(total_pages * page_size, chunk) + batch;
+}
+
+static WsLayout paged_layout(int64_t batch, int64_t Y, int gt, int64_t D, int64_t page_size,
+                             int64_t total_pages, int64_t chunk) {
+  return ws_layout(batch * Y, paged_grid_x(total_pages, page_size, chunk, batch) * Y, gt, D);
 }
 
 extern "C" size_t akt_decode_paged_workspace_size(int64_t batch, int64_t num_q_heads,
@@ -1207,20 +1335,17 @@ extern "C" size_t akt_decode_paged_workspace_size(int64_t batch, int64_t num_q_h
   const int gt = pick_gt(G, (int)head_dim);
   const int64_t Y = num_kv_heads * ceil_div(G, gt);
   const int64_t chunk = paged_chunk(chunk_tokens, total_pages, page_size, Y, batch);
-  return kCounterBytes +
-         split_ws_bytes(paged_grid_x(total_pages, page_size, chunk, batch) * Y, gt, head_dim);
+  return paged_layout(batch, Y, gt, head_dim, page_size, total_pages, chunk).total;
 }
 
-extern "C" int akt_decode_paged_fwd(const void* q, const void* kv_cache,
-                                    const int32_t* kv_page_indptr, const int32_t* kv_page_indices,
-                                    const int32_t* kv_last_page_len, void* o, float* lse,
-                                    int64_t batch, int64_t num_q_heads, int64_t num_kv_heads,
-                                    int64_t head_dim, int64_t page_size, int64_t total_pages,
-                                    int64_t num_pool_pages, const int64_t q_stride[4],
-                                    const int64_t kv_stride[5], float softmax_scale,
-                                    int64_t chunk_tokens, void* workspace,
-                                    size_t workspace_bytes, void* stream) {
-  clear_error();
+namespace akt {
+int paged_decode_impl(const void* q, const void* kv_cache, const int32_t* kv_page_indptr,
+                      const int32_t* kv_page_indices, const int32_t* kv_last_page_len, void* o,
+                      float* lse, int64_t batch, int64_t num_q_heads, int64_t num_kv_heads,
+                      int64_t head_dim, int64_t page_size, int64_t total_pages,
+                      int64_t num_pool_pages, const int64_t q_stride[4],
+                      const int64_t kv_stride[5], float softmax_scale, int64_t chunk_tokens,
+                      void* workspace, size_t workspace_bytes, void* stream) {
   int rc = check_common(batch, num_q_heads, num_kv_heads, head_dim);
   if (rc) return rc;
   AKT_CHECK(page_size > 0 && page_size < (1 << 20), "page_size out of range");
@@ -1238,9 +1363,9 @@ extern "C" int akt_decode_paged_fwd(const void* q, const void* kv_cache,
   const int64_t Y = num_kv_heads * n_hg;
   const int64_t chunk = paged_chunk(chunk_tokens, total_pages, page_size, Y, batch);
   const int64_t gx = paged_grid_x(total_pages, page_size, chunk, batch);
-  const size_t need = kCounterBytes + split_ws_bytes(gx * Y, gt, D);
-  if (!workspace || workspace_bytes < need)
-    return set_error(AKT_ERR_WORKSPACE, "workspace of %zu bytes required", need);
+  const WsLayout wl = paged_layout(batch, Y, gt, D, page_size, total_pages, chunk);
+  rc = check_workspace(wl, workspace, workspace_bytes);
+  if (rc) return rc;
 
   SplitParams p = {};
   p.q = (const half_t*)q;
@@ -1251,9 +1376,7 @@ extern "C" int akt_decode_paged_fwd(const void* q, const void* kv_cache,
   p.last_len = kv_last_page_len;
   p.o = (half_t*)o;
   p.lse = lse;
-  p.counters = (int*)workspace;
-  p.part_o = (float*)((char*)workspace + kCounterBytes);
-  p.part_ml = p.part_o + (size_t)gx * Y * gt * D;
+  bind_workspace(p, workspace, wl);
   p.q_sb = q_stride[0];
   p.q_sh = q_stride[1];
   p.k_sa = kv_stride[0]; p.k_sb = kv_stride[3]; p.k_head = kv_stride[2];
@@ -1265,10 +1388,30 @@ extern "C" int akt_decode_paged_fwd(const void* q, const void* kv_cache,
   p.chunk = (int)chunk;
   p.qk_scale = softmax_scale * kLog2e;
   hipStream_t st = (hipStream_t)stream;
-  dim3 grid((unsigned)gx, (unsigned)Y);
-  dim3 cgrid((unsigned)batch, (unsigned)Y);
-  if (page_size % 16 == 0) return launch_d<kModePaged, true, false>(D, gt, p, grid, cgrid, st);
-  return launch_d<kModePaged, false, false>(D, gt, p, grid, cgrid, st);
+  // grid.x >= batch: the non-persistent form writes empty sequences' rows from
+  // workgroups blockIdx.x < batch.
+  const dim3 grid((unsigned)gx, (unsigned)Y);
+  rc = clear_extra_arrivals(p, wl, st);
+  if (rc) return rc;
+  if (page_size % 16 == 0) return launch_d<kModePaged, true, false>(D, gt, p, grid, st);
+  return launch_d<kModePaged, false, false>(D, gt, p, grid, st);
+}
+}  // namespace akt
+
+extern "C" int akt_decode_paged_fwd(const void* q, const void* kv_cache,
+                                    const int32_t* kv_page_indptr, const int32_t* kv_page_indices,
+                                    const int32_t* kv_last_page_len, void* o, float* lse,
+                                    int64_t batch, int64_t num_q_heads, int64_t num_kv_heads,
+                                    int64_t head_dim, int64_t page_size, int64_t total_pages,
+                                    int64_t num_pool_pages, const int64_t q_stride[4],
+                                    const int64_t kv_stride[5], float softmax_scale,
+                                    int64_t chunk_tokens, void* workspace,
+                                    size_t workspace_bytes, void* stream) {
+  clear_error();
+  return paged_decode_impl(q, kv_cache, kv_page_indptr, kv_page_indices, kv_last_page_len, o, lse,
+                           batch, num_q_heads, num_kv_heads, head_dim, page_size, total_pages,
+                           num_pool_pages, q_stride, kv_stride, softmax_scale, chunk_tokens,
+                           workspace, workspace_bytes, stream);
 }
 
 // ----------------------------- sparse decode -------------------------------
@@ -1278,7 +1421,7 @@ extern "C" size_t akt_sparse_decode_workspace_size(int64_t batch, int64_t num_q_
   if (batch <= 0 || num_q_heads <= 0 || !head_dim_ok(head_dim)) return 0;
   const int64_t rows = batch * num_q_heads;
   const int64_t ns = num_splits > 0 ? num_splits : auto_splits(rows, l_max);
-  return kCounterBytes + (ns > 1 ? split_ws_bytes(rows * ns, 1, head_dim) : 0);
+  return ws_layout(rows, ns > 1 ? rows * ns : 0, 1, head_dim).total;
 }
 
 namespace {
@@ -1289,30 +1432,32 @@ int sparse_common(SplitParams& p, const void* q, const int32_t* sparse_ind,
                   int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim, int64_t l_max,
                   const int64_t q_stride[4], const int64_t ind_stride[2],
                   const int64_t nnz_stride[2], int64_t num_splits, void* workspace,
-                  size_t workspace_bytes, int64_t& ns_out) {
+                  size_t workspace_bytes, int64_t& ns_out, WsLayout& wl_out) {
   int rc = check_common(batch, num_q_heads, num_kv_heads, head_dim);
   if (rc) return rc;
   AKT_CHECK(l_max >= 0 && l_max < (1ll << 31), "l_max out of range");
   AKT_CHECK(q_stride[3] == 1, "head_dim stride must be 1");
   AKT_CHECK(rows_aligned16(q, q_stride, 2) && aligned16(o), "tensors must have 16-byte aligned rows");
   AKT_CHECK(num_splits >= 0, "num_splits must be >= 0");
+  ns_out = 0;
+  if (batch == 0) return AKT_OK;  // nothing to compute: no workspace needed
   const int64_t rows = batch * num_q_heads;
   const int64_t ns = num_splits > 0 ? num_splits : auto_splits(rows, l_max);
-  const size_t need = kCounterBytes + (ns > 1 ? split_ws_bytes(rows * ns, 1, head_dim) : 0);
-  if (!workspace || workspace_bytes < need)
-    return set_error(AKT_ERR_WORKSPACE, "workspace of %zu bytes required", need);
+  const WsLayout wl = ws_layout(rows, ns > 1 ? rows * ns : 0, 1, head_dim);
+  rc = check_workspace(wl, workspace, workspace_bytes);
+  if (rc) return rc;
+  wl_out = wl;
   p.q = (const half_t*)q;
   AKT_CHECK(csr_ptr || (sparse_nnz && (sparse_ind || l_max == 0) && ind_stride && nnz_stride),
             "kept-index pointers and strides are required");
-  AKT_CHECK(!csr_ptr || sparse_ind || batch == 0, "CSR kept indices are required");
+  AKT_CHECK(!csr_ptr || sparse_ind,
+            "CSR kept indices are required (a valid pointer even when every row is empty)");
   p.sparse_ind = sparse_ind;
   p.sparse_nnz = sparse_nnz;
   p.csr_ptr = csr_ptr;
   p.o = (half_t*)o;
   p.lse = lse;
-  p.counters = (int*)workspace;
-  p.part_o = (float*)((char*)workspace + kCounterBytes);
-  p.part_ml = p.part_o + (ns > 1 ? (size_t)rows * ns * head_dim : 0);
+  bind_workspace(p, workspace, wl);
   p.q_sb = q_stride[0];
   p.q_sh = q_stride[1];
   if (!csr_ptr) {
@@ -1343,9 +1488,10 @@ static int sparse_dense_impl(const void* q, const void* k, const void* v,
   clear_error();
   SplitParams p = {};
   int64_t ns = 0;
+  WsLayout wl = {};
   int rc = sparse_common(p, q, sparse_ind, sparse_nnz, csr_ptr, o, lse, batch, num_q_heads,
                          num_kv_heads, head_dim, l_max, q_stride, ind_stride, nnz_stride,
-                         num_splits, workspace, workspace_bytes, ns);
+                         num_splits, workspace, workspace_bytes, ns, wl);
   if (rc) return rc;
   AKT_CHECK(seq_len >= 0 && seq_len < (1ll << 31), "seq_len out of range");
   AKT_CHECK(k_stride[3] == 1 && v_stride[3] == 1, "head_dim stride must be 1");
@@ -1359,9 +1505,10 @@ static int sparse_dense_impl(const void* q, const void* k, const void* v,
   p.S = (int)seq_len;
   p.qk_scale = softmax_scale * kLog2e;
   const int64_t rows = batch * num_q_heads;
-  dim3 grid((unsigned)(rows * ns), 1);
-  dim3 cgrid(ns > 1 ? (unsigned)rows : 0u, 1);
-  return launch_d<kModeSparseDense, false, false>((int)head_dim, 1, p, grid, cgrid,
+  rc = clear_extra_arrivals(p, wl, (hipStream_t)stream);
+  if (rc) return rc;
+  return launch_d<kModeSparseDense, false, false>((int)head_dim, 1, p,
+                                                  dim3((unsigned)(rows * ns), 1),
                                                   (hipStream_t)stream);
 }
 
@@ -1411,9 +1558,10 @@ static int sparse_paged_impl(bool magic, const void* q, const void* kv_cache,
   clear_error();
   SplitParams p = {};
   int64_t ns = 0;
+  WsLayout wl = {};
   int rc = sparse_common(p, q, sparse_ind, sparse_nnz, csr_ptr, o, lse, batch, num_q_heads,
                          num_kv_heads, head_dim, l_max, q_stride, ind_stride, nnz_stride,
-                         num_splits, workspace, workspace_bytes, ns);
+                         num_splits, workspace, workspace_bytes, ns, wl);
   if (rc) return rc;
   AKT_CHECK(page_size > 0 && page_size < (1 << 20), "page_size out of range");
   AKT_CHECK(num_pool_pages >= 0, "num_pool_pages out of range");
@@ -1434,11 +1582,12 @@ static int sparse_paged_impl(bool magic, const void* q, const void* kv_cache,
   p.lsh_k = lsh_k;
   p.lsh_l = lsh_l;
   const int64_t rows = batch * num_q_heads;
-  dim3 grid((unsigned)(rows * ns), 1);
-  dim3 cgrid(ns > 1 ? (unsigned)rows : 0u, 1);
+  const dim3 grid((unsigned)(rows * ns), 1);
   hipStream_t st = (hipStream_t)stream;
-  if (magic) return launch_d<kModeSparsePaged, false, true>((int)head_dim, 1, p, grid, cgrid, st);
-  return launch_d<kModeSparsePaged, false, false>((int)head_dim, 1, p, grid, cgrid, st);
+  rc = clear_extra_arrivals(p, wl, st);
+  if (rc) return rc;
+  if (magic) return launch_d<kModeSparsePaged, false, true>((int)head_dim, 1, p, grid, st);
+  return launch_d<kModeSparsePaged, false, false>((int)head_dim, 1, p, grid, st);
 }
 
 extern "C" int akt_sparse_decode_paged_fwd(

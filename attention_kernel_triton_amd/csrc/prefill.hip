@@ -71,8 +71,6 @@ constexpr int kSlots = 4;   // waves per workgroup
 constexpr int kRows = 64;   // query rows per slot (two 32-row MFMA blocks)
 constexpr int kBN = 64;     // keys per staged tile
 constexpr int kNBuf = 4;    // LDS tile buffers
-// Word 3 of a raw (stride 0) gfx9 buffer resource: 32-bit data format.
-constexpr int kBufferWord3 = 0x00020000;
 constexpr float kRescaleSlack = 8.0f;
 // Largest row sum of one 32-key step that lets P stay unchecked: below it
 // every probability is under 32 * 2^kRescaleSlack, far inside fp16's range;

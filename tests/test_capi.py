@@ -78,15 +78,30 @@ def test_sparse_rejects_unaligned_rows():
     assert rc == 1 and b"aligned" in lib.akt_last_error()
 
 
+def _ws(units, parts, gt, D):
+    """Split-KV workspace layout: a 256-byte counter header; with partials, at
+    least 32768 int32 arrival counters (one per unit), fp32 partial outputs
+    [parts, gt, D] and their (m, l, e, pad) rows [parts, gt, 4], each array
+    padded to 256 bytes."""
+    if parts == 0:
+        return 256
+    ru = lambda x: -(-x // 256) * 256  # noqa: E731
+    return 256 + ru(max(units, 32768) * 4) + ru(parts * gt * D * 4) + parts * gt * 16
+
+
 def test_workspace_sizes_scale_with_problem():
     lib = N.load()
     a = lib.akt_decode_paged_workspace_size(32, 32, 8, 128, 16, 8448, 0)
     b = lib.akt_decode_paged_workspace_size(32, 32, 8, 128, 16, 2 * 8448, 0)
     assert 0 < a <= b
-    # 256-byte counter header, plus partials only when a unit has several chunks
-    assert lib.akt_decode_workspace_size(8, 64, 16, 512, 64, 512) == 256
-    assert lib.akt_sparse_decode_workspace_size(1, 32, 128, 3840, 1) == 256
-    assert lib.akt_sparse_decode_workspace_size(1, 32, 128, 3840, 8) == 256 + 32 * 8 * 132 * 4
+    # partials only when a unit has several chunks (8 x 16 units of 4 heads here)
+    assert lib.akt_decode_workspace_size(8, 64, 16, 512, 64, 512) == _ws(128, 0, 4, 64) == 256
+    assert lib.akt_decode_workspace_size(8, 64, 16, 1024, 64, 512) == _ws(128, 256, 4, 64)
+    assert lib.akt_decode_workspace_size(4000, 64, 16, 1024, 64, 512) == _ws(64000, 128000, 4, 64)
+    assert lib.akt_sparse_decode_workspace_size(1, 32, 128, 3840, 1) == _ws(32, 0, 1, 128)
+    assert lib.akt_sparse_decode_workspace_size(1, 32, 128, 3840, 8) == _ws(32, 256, 1, 128)
+    # nothing to compute: no workspace
+    assert lib.akt_sparse_decode_workspace_size(0, 32, 128, 3840, 0) == 0
 
 
 def test_automatic_chunk_length():
@@ -111,11 +126,11 @@ def test_automatic_sparse_split_count():
     at most one per 64 index slots of l_max; the workspace size shows the count."""
     lib = N.load()
     ws = lib.akt_sparse_decode_workspace_size
-    part = lambda rows, ns, D: 256 + rows * ns * (D + 4) * 4
+    part = lambda rows, ns, D: _ws(rows, rows * ns if ns > 1 else 0, 1, D)  # noqa: E731
     assert ws(1, 32, 128, 3840, 0) == part(32, 16, 128)      # config 4a: 512 / 32 rows
     assert ws(3, 32, 256, 32768, 0) == part(96, 5, 256)      # config 4b: 512 / 96 rows
     assert ws(1, 32, 128, 200, 0) == part(32, 4, 128)        # capped at ceil(200 / 64)
-    assert ws(64, 32, 128, 3840, 0) == 256                   # 2048 rows: one split, no partials
+    assert ws(64, 32, 128, 3840, 0) == part(2048, 1, 128)    # 2048 rows: one split, no partials
 
 
 def test_kept_index_rejects_short_row_stride():

@@ -261,3 +261,66 @@ def test_decode_long_sequence(dev):
     ro, rl = naive.decode(q, K, V, 1 / math.sqrt(128), 4)
     assert_close(o, ro, what="decode S=131072")
     assert_close(lse, rl, atol=1e-4, what="decode S=131072 lse")
+
+
+@pytest.mark.parametrize("page", [16, 8])
+def test_paged_batch_past_the_lds_chunk_table(dev, page):
+    """Batches over 1024 sequences take the non-persistent kernel: each workgroup
+    locates its chunk by scanning the page table, chunks are 256 tokens, and the
+    first workgroups write the rows of empty sequences.  Both the page-aligned
+    (16) and the unaligned (8) group addressing are covered, with the LSE."""
+    g = torch.Generator().manual_seed(40 + page)
+    B, Hq, Hkv, D = 1100, 4, 2, 128
+    lens = torch.randint(1, 700, (B,), generator=g).tolist()
+    for b in (0, 3, 517, B - 1):
+        lens[b] = 0
+    indptr, indices, last, P = syn.block_table(g, lens, page, extra_pages=5)
+    pool = torch.randn(P, 2, Hkv, page, D, generator=g).half()
+    q = torch.randn(B, Hq, 1, D, generator=g).half()
+    o, lse = pg.flash_attention_decode_paged(q.to(dev), pool.to(dev), indptr.to(dev),
+                                             indices.to(dev), last.to(dev), return_lse=True)
+    ro, rl = naive.naive_paged_attention(q, pool, indptr, indices, last)
+    nonempty = torch.tensor(lens) > 0
+    assert_close(o, ro, what=f"paged B={B} page={page}")
+    assert_close(lse, rl, atol=1e-4, what="paged lse", mask=nonempty)
+    assert torch.isinf(lse.cpu()[~nonempty]).all()
+
+
+def test_paged_merges_are_coherent_across_launches(dev):
+    """The last workgroup of a unit merges partials other workgroups (on any XCD)
+    stored in the same launch.  Alternating two inputs over one workspace, every
+    launch must reproduce its input's first result bit for bit: a partial read
+    before it was visible, or a stale one from the previous launch, would not."""
+    a = syn.paged_config(B=32, min_len=256, max_len=8192).to(dev)
+    b = syn.paged_config(seed=7, B=32, min_len=256, max_len=8192).to(dev)
+    ra = pg.flash_attention_decode_paged(a.q, a.pool, a.indptr, a.indices, a.last_len)
+    rb = pg.flash_attention_decode_paged(b.q, b.pool, b.indptr, b.indices, b.last_len)
+    outs = []
+    for _ in range(10):
+        outs.append((pg.flash_attention_decode_paged(a.q, a.pool, a.indptr, a.indices,
+                                                     a.last_len),
+                     pg.flash_attention_decode_paged(b.q, b.pool, b.indptr, b.indices,
+                                                     b.last_len)))
+    for oa, ob in outs:
+        assert torch.equal(oa, ra) and torch.equal(ob, rb)
+    ref, _ = naive.naive_paged_attention(a.q.cpu(), a.pool.cpu(), a.indptr.cpu(),
+                                         a.indices.cpu(), a.last_len.cpu())
+    assert_close(ra, ref, what="config-3-sized merge")
+
+
+def test_decode_more_units_than_the_fixed_arrival_area(dev):
+    """35200 units (B = 1100, 32 kv heads, G = 1, two chunks each).  Arrival
+    counters past the fixed 32768-slot area sit where the earlier, smaller calls
+    stored their partials, so the call must clear them first.  Splitting the
+    batch does not change what any unit computes, so the results are bit-identical."""
+    g = torch.Generator().manual_seed(50)
+    B, Hkv, S, D = 1100, 32, 150, 64
+    q = torch.randn(B, Hkv, 1, D, generator=g).half().to(dev)
+    K = torch.randn(B, Hkv, S, D, generator=g).half().to(dev)
+    V = torch.randn(B, Hkv, S, D, generator=g).half().to(dev)
+    parts = [_ops.decode(q[i:i + 100], K[i:i + 100], V[i:i + 100], 0.125, chunk_tokens=128)
+             for i in range(0, B, 100)]
+    full = _ops.decode(q, K, V, 0.125, chunk_tokens=128)
+    assert torch.equal(full, torch.cat(parts))
+    ro, _ = naive.decode(q[:100].cpu(), K[:100].cpu(), V[:100].cpu(), 0.125, 1)
+    assert_close(parts[0], ro, what="first slice")

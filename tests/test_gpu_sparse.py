@@ -234,3 +234,31 @@ def test_sparse_paged_page_ids_past_32_bit_byte_offsets(dev):
     assert_close(o, ro, what="sparse paged, page ids near 70000")
     assert_close(lse, rl, atol=1e-4, what="sparse paged lse, page ids near 70000")
     del pool
+
+
+def test_sparse_empty_batch_returns_empty_outputs(dev):
+    """B = 0: nothing to compute, no workspace; both sparse entry points return
+    empty outputs (as dense and paged decode do)."""
+    q = torch.zeros(0, 8, 1, 128, dtype=torch.float16, device=dev)
+    K = torch.zeros(0, 2, 64, 128, dtype=torch.float16, device=dev)
+    ind = torch.zeros(0, 8, 16, dtype=torch.int32, device=dev)
+    nnz = torch.zeros(0, 8, 1, dtype=torch.int32, device=dev)
+    o, lse = sp.sparsetoken_flash_attention_decode(q, K, K, ind, nnz, 0.1, 4, return_lse=True)
+    assert o.shape == (0, 8, 1, 128) and lse.shape == (0, 8)
+    pool = torch.zeros(4, 2, 2, 16, 128, dtype=torch.float16, device=dev)
+    indptr = torch.zeros(1, dtype=torch.int32, device=dev)
+    pages = torch.zeros(0, dtype=torch.int32, device=dev)
+    o2 = spp.sparsetoken_flash_attention_decode_paged(q, pool, indptr, pages, ind, nnz)
+    assert o2.shape == (0, 8, 128)
+
+
+def test_sparse_splits_merge_deterministically(dev):
+    """Split partials are merged by whichever workgroup of a row finishes last;
+    the merge order is fixed, so repeated calls are bit-identical."""
+    s = syn.sparse_config()
+    ind, nnz = _sparse_lists(s)
+    args = (s.q.to(dev), s.K.to(dev), s.V.to(dev), ind.to(dev), nnz.to(dev), s.scale, s.group)
+    o0, l0 = sp.sparsetoken_flash_attention_decode(*args, return_lse=True)
+    for _ in range(5):
+        o, lse = sp.sparsetoken_flash_attention_decode(*args, return_lse=True)
+        assert torch.equal(o, o0) and torch.equal(lse, l0)

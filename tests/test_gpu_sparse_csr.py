@@ -100,3 +100,16 @@ def test_sparse_paged_and_magicpig_csr_equal_padded(dev):
     r64, _ = naive.magicpig_sparsetoken_naive_paged_attention(p.q, p.pool, p.indptr, p.indices,
                                                               ind, nnz, s.lsh_k, s.lsh_l)
     assert_close(o3, r64, what="MagicPIG CSR vs fp64 oracle")
+
+
+def test_sparse_csr_every_row_empty(dev):
+    """A CSR call whose rows are all empty (inds has no entries): zeros and -inf."""
+    B, Hq, Hkv, S, D = 1, 4, 2, 100, 128
+    q = torch.randn(B, Hq, 1, D).half().to(dev)
+    K = torch.randn(B, Hkv, S, D).half().to(dev)
+    inds = torch.zeros(0, dtype=torch.int32, device=dev)
+    ptr = torch.zeros(B * Hq + 1, dtype=torch.int64, device=dev)
+    for splits in (1, 3):
+        o, lse = _ops.sparse_decode_csr(q, K, K, inds, ptr, 0.1, return_lse=True,
+                                        num_splits=splits)
+        assert torch.equal(o.cpu(), torch.zeros_like(o.cpu())) and torch.isinf(lse.cpu()).all()
