@@ -38,6 +38,9 @@ _SIGNATURES = {
     "akt_decode_paged_workspace_size": (C.c_size_t, [_i64, _i64, _i64, _i64, _i64, _i64, _i64]),
     "akt_decode_paged_fwd": (C.c_int, [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64,
                                        _i64, _i64, _i64x, _i64x, C.c_float, _i64, _p, C.c_size_t, _p]),
+    "akt_decode_paged_fwd_noalloc": (C.c_int, [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64,
+                                               _i64, _i64, _i64, _i64x, _i64x, C.c_float, _i64,
+                                               _p]),
     "akt_sparse_decode_workspace_size": (C.c_size_t, [_i64, _i64, _i64, _i64, _i64]),
     "akt_sparse_decode_fwd": (C.c_int, [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64,
                                         _i64, _i64x, _i64x, _i64x, _i64x, _i64x, C.c_float, _i64,

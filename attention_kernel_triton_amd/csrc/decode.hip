@@ -33,6 +33,7 @@
 #include <math.h>
 
 #include <atomic>
+#include <mutex>
 
 #include "akt_common.hpp"
 #include "akt_host.hpp"
@@ -1637,4 +1638,75 @@ extern "C" int akt_sparse_decode_paged_csr_fwd(
                            page_size, num_pool_pages, max_nnz, q_stride, kv_stride, nullptr,
                            nullptr, 1.0f / sqrtf((float)head_dim), num_splits, workspace,
                            workspace_bytes, stream);
+}
+
+// ----------------------------- no-allocation paged decode ------------------
+// akt_decode_paged_fwd_noalloc keeps its split-KV workspace in this
+// file-scope device array instead of caller memory: each GPU the library
+// runs on holds its own copy, at its own address, until the process ends.
+// In host code the name `scratch` is only a stand-in for the symbol; the
+// device address comes from hipGetSymbolAddress (per device, with that device
+// current) and only that address is ever passed to a kernel.
+static __device__ __align__(256) unsigned char scratch[AKT_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices];  // device address of `scratch`, per device (guarded)
+
+// Device address of `scratch` on the current device.  The first call on a
+// device looks it up and zero-fills the workspace's counter area (the
+// scheduling counters and the fixed arrival counters, which every launch
+// leaves at zero again) with a fill kernel on `st`, ahead of the first launch
+// that uses it.
+int scratch_for_current_device(hipStream_t st, void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return set_error(AKT_ERR_HIP, "hipGetDevice failed: %s", hipGetErrorString(e));
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr)
+      return set_error(AKT_ERR_HIP, "hipGetSymbolAddress(scratch) failed: %s",
+                       hipGetErrorString(e));
+    const int64_t n = (int64_t)((kCounterBytes + kArriveSlots * 4) / 4);
+    hipLaunchKernelGGL(zero_words_kernel, dim3((unsigned)ceil_div(n, kThreads)), dim3(kThreads), 0,
+                       st, (int*)ptr, n);
+    const int rc = check_launch("zero_words_kernel");
+    if (rc) return rc;
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return AKT_OK;
+}
+}  // namespace
+
+extern "C" int akt_decode_paged_fwd_noalloc(
+    const void* q, const void* kv_cache, const int32_t* kv_page_indptr,
+    const int32_t* kv_page_indices, const int32_t* kv_last_page_len, void* o, float* lse,
+    int64_t batch, int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim, int64_t page_size,
+    int64_t total_pages, int64_t num_pool_pages, const int64_t q_stride[4],
+    const int64_t kv_stride[5], float softmax_scale, int64_t chunk_tokens, void* stream) {
+  clear_error();
+  // Invalid arguments size to 0 here and are reported by paged_decode_impl.
+  const size_t need = akt_decode_paged_workspace_size(batch, num_q_heads, num_kv_heads, head_dim,
+                                                      page_size, total_pages, chunk_tokens);
+  if (need > (size_t)AKT_NOALLOC_SCRATCH_BYTES)
+    return set_error(AKT_ERR_INVALID_ARGUMENT,
+                     "this call needs %zu bytes of split-KV workspace; the no-allocation entry "
+                     "point holds %zu (use akt_decode_paged_fwd with a caller workspace)",
+                     need, (size_t)AKT_NOALLOC_SCRATCH_BYTES);
+  if (batch == 0) return paged_decode_impl(q, kv_cache, kv_page_indptr, kv_page_indices,
+                                           kv_last_page_len, o, lse, batch, num_q_heads,
+                                           num_kv_heads, head_dim, page_size, total_pages,
+                                           num_pool_pages, q_stride, kv_stride, softmax_scale,
+                                           chunk_tokens, nullptr, 0, stream);
+  void* ws = nullptr;
+  const int rc = scratch_for_current_device((hipStream_t)stream, &ws);
+  if (rc) return rc;
+  return paged_decode_impl(q, kv_cache, kv_page_indptr, kv_page_indices, kv_last_page_len, o, lse,
+                           batch, num_q_heads, num_kv_heads, head_dim, page_size, total_pages,
+                           num_pool_pages, q_stride, kv_stride, softmax_scale, chunk_tokens, ws,
+                           (size_t)AKT_NOALLOC_SCRATCH_BYTES, stream);
 }

@@ -168,6 +168,30 @@ int akt_decode_paged_fwd(const void* q, const void* kv_cache, const int32_t* kv_
                          void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * akt_decode_paged_fwd without a workspace argument: no reference
+ * counterpart.  It is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc), and it allocates nothing.  The split-KV workspace is a
+ * file-scope device array of AKT_NOALLOC_SCRATCH_BYTES that every GPU the
+ * library runs on holds until the process ends; its counter area is
+ * zero-filled (by a fill kernel on `stream`) at the first call on a device,
+ * and every launch leaves its counters at zero again.  A call whose workspace
+ * (akt_decode_paged_workspace_size of the same arguments) exceeds the array
+ * fails with AKT_ERR_INVALID_ARGUMENT.  All calls on one GPU share the array:
+ * calls that overlap in time on one GPU race, so order them (one stream).
+ * Results are bit-identical to akt_decode_paged_fwd's.
+ */
+#define AKT_NOALLOC_SCRATCH_BYTES (32u << 20)
+int akt_decode_paged_fwd_noalloc(const void* q, const void* kv_cache,
+                                 const int32_t* kv_page_indptr, const int32_t* kv_page_indices,
+                                 const int32_t* kv_last_page_len, void* o, float* lse,
+                                 int64_t batch, int64_t num_q_heads, int64_t num_kv_heads,
+                                 int64_t head_dim, int64_t page_size, int64_t total_pages,
+                                 int64_t num_pool_pages, const int64_t q_stride[4],
+                                 const int64_t kv_stride[5], float softmax_scale,
+                                 int64_t chunk_tokens, void* stream);
+
+/*
  * Sparse-token decode over a dense cache.  Replaces
  * sparsetoken_decode_flash_attention_redundant.py:127.
  *   sparse_ind: [batch, num_q_heads, l_max] int32 kept token indices

@@ -198,3 +198,17 @@ def test_paged_append_validates_arguments():
     rc = lib.akt_paged_kv_append(None, None, None, None, None, None, None, 1, 0, 2, 64, 16, 8, s3,
                                  s3, s5, None)
     assert rc == 0  # nothing to append
+
+
+def test_noalloc_paged_decode_rejects_workspace_past_its_array():
+    """The no-allocation entry point refuses, before any GPU call, a problem whose
+    split-KV workspace exceeds its fixed device array (32 MiB)."""
+    lib = N.load()
+    need = lib.akt_decode_paged_workspace_size(256, 32, 8, 128, 16, 400000, 0)
+    assert need > 32 << 20
+    qs, kvs = _i64(32 * 128, 128, 128, 1), _i64(2 * 8 * 16 * 128, 8 * 16 * 128, 16 * 128, 128, 1)
+    rc = lib.akt_decode_paged_fwd_noalloc(C.c_void_p(16), C.c_void_p(16), C.c_void_p(16),
+                                          C.c_void_p(16), C.c_void_p(16), C.c_void_p(16), None,
+                                          256, 32, 8, 128, 16, 400000, 400000, qs, kvs, 0.088, 0,
+                                          None)
+    assert rc == 1 and b"no-allocation" in lib.akt_last_error()
