@@ -83,13 +83,34 @@ def load() -> C.CDLL:
         raise RuntimeError(
             f"{path} is not built: run `python -m attention_kernel_triton_amd.build` "
             "(the HIP kernels have no fallback implementation)")
-    lib = C.CDLL(str(path))
+    # Global symbols: the compiled host layer (_akt_torch) resolves its akt_*
+    # calls against this library.
+    lib = C.CDLL(str(path), mode=C.RTLD_GLOBAL)
     for name, (res, args) in _SIGNATURES.items():
         fn = getattr(lib, name)
         fn.restype = res
         fn.argtypes = args
     _lib = lib
     return lib
+
+
+_ext = None
+
+
+def torch_ext():
+    """The compiled host layer of the hot entry points (module ``_akt_torch``,
+    built from csrc/torch_ops.cpp), loaded after libakt_amd.so."""
+    global _ext
+    if _ext is None:
+        load()
+        try:
+            from . import _akt_torch
+        except ImportError as e:
+            raise RuntimeError(
+                "the host layer _akt_torch is not built: run "
+                "`python -m attention_kernel_triton_amd.build`") from e
+        _ext = _akt_torch
+    return _ext
 
 
 def exported_symbols() -> list[str]:
@@ -158,6 +179,15 @@ def workspace(nbytes: int, device, stream=None) -> torch.Tensor | None:
         buf = torch.zeros(size, dtype=torch.uint8, device=dev)
         _WS_CACHE[key] = buf
     return buf
+
+
+def workspace_buffers():
+    """(device index, stream handle, buffer) of every cached decode workspace:
+    those of the Python wrappers (``workspace``) and of the compiled host layer."""
+    out = [(k[0], k[1] or 0, v) for k, v in _WS_CACHE.items()]
+    if _ext is not None:
+        out += [(d, s, b) for d, s, b in _ext.workspaces()]
+    return out
 
 
 class kernel_timer:

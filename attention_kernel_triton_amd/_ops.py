@@ -3,11 +3,11 @@
 Each function validates devices, dtypes and layouts, allocates outputs and the
 split-KV workspace through torch's caching allocator, and launches on the
 current HIP stream of the input's device.  They never synchronise and never
-fall back to another implementation.
+fall back to another implementation.  The hot entry points run in the
+compiled host layer (_akt_torch); the rest bind the C ABI through ctypes.
 """
 from __future__ import annotations
 
-import math
 
 import torch
 
@@ -46,43 +46,31 @@ def _same_device(dev, **tensors) -> None:
             raise ValueError(f"{name} is on {t.device}, expected {dev}")
 
 
-# --------------------------------------------------------------------------- prefill
-def prefill(Q, K, V, causal: bool, softmax_scale: float, varlen=None, return_lse: bool = False):
+# --------------------------------------------------------------------------- hot paths
+# prefill, decode, decode_paged, sparse_decode and sparse_decode_paged run in
+# the compiled host layer (csrc/torch_ops.cpp): the same checks, allocation,
+# stream and workspace handling as the wrappers below, at a few microseconds
+# of host time per call.  The first call of each name binds this module's
+# attribute to the compiled function.
+_HOT = ("prefill", "decode", "decode_paged", "sparse_decode", "sparse_decode_paged")
+
+
+def _hot(name):
+    ext = N.torch_ext()
+    g = globals()
+    for n in _HOT:
+        g[n] = getattr(ext, n)
+    return getattr(ext, name)
+
+
+def prefill(Q, K, V, causal, softmax_scale, varlen=None, return_lse=False):
     """O = softmax(scale * Q K^T [+ causal mask]) V for Q [B,Hq,S,D], K/V [B,Hkv,S,D].
 
-    With return_lse, also the fp32 natural-log normaliser [B, Hq, S] of every
+    varlen: optional device int32/int64 [B] of valid lengths.  With
+    return_lse, also the fp32 natural-log normaliser [B, Hq, S] of every
     computed row (rows a var-len call leaves unwritten stay uninitialised).
     """
-    Q = _half_rows("Q", Q)
-    K = _half_rows("K", K)
-    V = _half_rows("V", V)
-    _same_device(Q.device, K=K, V=V)
-    B, H, S, D = Q.shape
-    O = torch.empty((B, H, S, D), dtype=Q.dtype, device=Q.device)
-    vptr, vbits = None, 0
-    if varlen is not None:
-        _need_gpu("varlen", varlen)
-        if varlen.dtype not in (torch.int32, torch.int64):
-            raise TypeError(f"varlen must be int32 or int64, got {varlen.dtype}")
-        if varlen.numel() != B:
-            raise ValueError(f"varlen must have {B} entries, got {varlen.numel()}")
-        varlen = varlen.contiguous()
-        vptr, vbits = N.ptr(varlen), (64 if varlen.dtype == torch.int64 else 32)
-    lib = N.load()
-    if return_lse:
-        lse = torch.empty((B, H, S), dtype=torch.float32, device=Q.device)
-        rc = lib.akt_prefill_fwd_lse(N.ptr(Q), N.ptr(K), N.ptr(V), N.ptr(O), N.ptr(lse), B, H,
-                                     K.shape[1], S, D, N.strides(Q), N.strides(K), N.strides(V),
-                                     N.strides(O), N.strides(lse), float(softmax_scale),
-                                     1 if causal else 0, vptr, vbits, N.stream_of(Q))
-        N.check(rc, "akt_prefill_fwd_lse")
-        return O, lse
-    rc = lib.akt_prefill_fwd(N.ptr(Q), N.ptr(K), N.ptr(V), N.ptr(O), B, H, K.shape[1], S, D,
-                             N.strides(Q), N.strides(K), N.strides(V), N.strides(O),
-                             float(softmax_scale), 1 if causal else 0, vptr, vbits,
-                             N.stream_of(Q))
-    N.check(rc, "akt_prefill_fwd")
-    return O
+    return _hot("prefill")(Q, K, V, causal, softmax_scale, varlen=varlen, return_lse=return_lse)
 
 
 # --------------------------------------------------------------------------- merge
@@ -131,146 +119,35 @@ def merge_states(o, lse, out_dtype=None):
 
 
 # --------------------------------------------------------------------------- decode
-def decode(q, K, V, softmax_scale: float, return_lse: bool = False, chunk_tokens: int = 0):
+def decode(q, K, V, softmax_scale, return_lse=False, chunk_tokens=0):
     """Single-query GQA decode: q [B,Hq,1,D], K/V [B,Hkv,S,D] -> o [B,Hq,1,D] (, lse [B,Hq])."""
-    q = _half_rows("q", q)
-    K = _half_rows("K", K)
-    V = _half_rows("V", V)
-    _same_device(q.device, K=K, V=V)
-    B, Hq, _, D = q.shape
-    Hkv, S = K.shape[1], K.shape[2]
-    o = torch.empty((B, Hq, 1, D), dtype=q.dtype, device=q.device)
-    lse = torch.empty((B, Hq), dtype=torch.float32, device=q.device) if return_lse else None
-    lib = N.load()
-    ws_n = lib.akt_decode_workspace_size(B, Hq, Hkv, S, D, chunk_tokens)
-    st = N.stream_of(q)
-    ws = N.workspace(ws_n, q.device, st)
-    rc = lib.akt_decode_fwd(N.ptr(q), N.ptr(K), N.ptr(V), N.ptr(o), N.ptr(lse), B, Hq, Hkv, S, D,
-                            N.strides(q), N.strides(K), N.strides(V), float(softmax_scale),
-                            chunk_tokens, N.ptr(ws), ws_n, st)
-    N.check(rc, "akt_decode_fwd")
-    return (o, lse) if return_lse else o
+    return _hot("decode")(q, K, V, softmax_scale, return_lse=return_lse,
+                          chunk_tokens=chunk_tokens)
 
 
 def decode_paged(q, paged_kv_cache, kv_page_indptr, kv_page_indices, kv_last_page_len,
-                 softmax_scale: float | None = None, return_lse: bool = False,
-                 chunk_tokens: int = 0):
+                 softmax_scale=None, return_lse=False, chunk_tokens=0):
     """Paged decode: q [B,Hq,1,D] (or [B,Hq,D]), pool [P,2,Hkv,page,D] -> o [B,Hq,D]."""
-    q = _half_rows("q", q)
-    pool = _half_rows("paged_kv_cache", paged_kv_cache)
-    dev = q.device
-    _same_device(dev, paged_kv_cache=pool)
-    indptr = _int32("kv_page_indptr", kv_page_indptr, dev)
-    indices = _int32("kv_page_indices", kv_page_indices, dev)
-    last = _int32("kv_last_page_len", kv_last_page_len, dev)
-    indptr, indices, last = indptr.contiguous(), indices.contiguous(), last.contiguous()
-    B, Hq, D = q.shape[0], q.shape[1], q.shape[-1]
-    q4 = q if q.dim() == 4 else q.unsqueeze(2)
-    P, _, Hkv, page, Dc = pool.shape
-    if Dc != D:
-        raise ValueError(f"head_dim mismatch: q has {D}, cache has {Dc}")
-    if indptr.numel() != B + 1 or last.numel() != B:
-        raise ValueError("kv_page_indptr must have B+1 and kv_last_page_len B entries")
-    scale = float(1.0 / math.sqrt(D)) if softmax_scale is None else float(softmax_scale)
-    o = torch.empty((B, Hq, D), dtype=q.dtype, device=dev)
-    lse = torch.empty((B, Hq), dtype=torch.float32, device=dev) if return_lse else None
-    total = indices.numel()
-    lib = N.load()
-    ws_n = lib.akt_decode_paged_workspace_size(B, Hq, Hkv, D, page, total, chunk_tokens)
-    st = N.stream_of(q)
-    ws = N.workspace(ws_n, dev, st)
-    rc = lib.akt_decode_paged_fwd(N.ptr(q4), N.ptr(pool), N.ptr(indptr), N.ptr(indices),
-                                  N.ptr(last), N.ptr(o), N.ptr(lse), B, Hq, Hkv, D, page, total,
-                                  P, N.strides(q4), N.strides(pool), scale, chunk_tokens,
-                                  N.ptr(ws), ws_n, st)
-    N.check(rc, "akt_decode_paged_fwd")
-    return (o, lse) if return_lse else o
+    return _hot("decode_paged")(q, paged_kv_cache, kv_page_indptr, kv_page_indices,
+                                kv_last_page_len, softmax_scale=softmax_scale,
+                                return_lse=return_lse, chunk_tokens=chunk_tokens)
 
 
-def _sparse_meta(sparse_ind, sparse_nnz, dev, B, Hq):
-    ind = _int32("sparse_ind", sparse_ind, dev)
-    nnz = _int32("sparse_nnz", sparse_nnz, dev)
-    if ind.dim() != 3 or ind.shape[0] != B or ind.shape[1] != Hq:
-        raise ValueError(f"sparse_ind must be [B={B}, H={Hq}, L_max], got {tuple(ind.shape)}")
-    if ind.stride(2) != 1:
-        ind = ind.contiguous()
-    if nnz.shape[0] != B or nnz.shape[1] != Hq or (nnz.dim() == 3 and nnz.shape[2] != 1):
-        raise ValueError(f"sparse_nnz must be [B={B}, H={Hq}(, 1)], got {tuple(nnz.shape)}")
-    return ind, nnz, N.i64s(ind.stride(0), ind.stride(1)), N.i64s(nnz.stride(0), nnz.stride(1))
-
-
-def sparse_decode(q, K, V, sparse_ind, sparse_nnz, softmax_scale: float,
-                  return_lse: bool = False, num_splits: int = 0):
+def sparse_decode(q, K, V, sparse_ind, sparse_nnz, softmax_scale, return_lse=False,
+                  num_splits=0):
     """Sparse-token decode over dense K/V: returns o [B,Hq,1,D] (, lse [B,Hq])."""
-    q = _half_rows("q", q)
-    K = _half_rows("K", K)
-    V = _half_rows("V", V)
-    dev = q.device
-    _same_device(dev, K=K, V=V)
-    B, Hq, _, D = q.shape
-    Hkv, S = K.shape[1], K.shape[2]
-    ind, nnz, ist, nst = _sparse_meta(sparse_ind, sparse_nnz, dev, B, Hq)
-    L = ind.shape[2]
-    o = torch.empty((B, Hq, 1, D), dtype=q.dtype, device=dev)
-    lse = torch.empty((B, Hq), dtype=torch.float32, device=dev) if return_lse else None
-    lib = N.load()
-    ws_n = lib.akt_sparse_decode_workspace_size(B, Hq, D, L, num_splits)
-    st = N.stream_of(q)
-    ws = N.workspace(ws_n, dev, st)
-    rc = lib.akt_sparse_decode_fwd(N.ptr(q), N.ptr(K), N.ptr(V), N.ptr(ind), N.ptr(nnz),
-                                   N.ptr(o), N.ptr(lse), B, Hq, Hkv, S, D, L, N.strides(q),
-                                   N.strides(K), N.strides(V), ist, nst, float(softmax_scale),
-                                   num_splits, N.ptr(ws), ws_n, st)
-    N.check(rc, "akt_sparse_decode_fwd")
-    return (o, lse) if return_lse else o
+    return _hot("sparse_decode")(q, K, V, sparse_ind, sparse_nnz, softmax_scale,
+                                 return_lse=return_lse, num_splits=num_splits)
 
 
 def sparse_decode_paged(q, paged_kv_cache, kv_page_indptr, kv_page_indices, sparse_ind,
-                        sparse_nnz, softmax_scale: float | None = None, return_lse: bool = False,
-                        num_splits: int = 0, lsh_k=None, lsh_l=None):
+                        sparse_nnz, softmax_scale=None, return_lse=False, num_splits=0,
+                        lsh_k=None, lsh_l=None):
     """Sparse-token paged decode (plain, or MagicPIG when lsh_k/lsh_l are given)."""
-    q = _half_rows("q", q)
-    pool = _half_rows("paged_kv_cache", paged_kv_cache)
-    dev = q.device
-    _same_device(dev, paged_kv_cache=pool)
-    indptr = _int32("kv_page_indptr", kv_page_indptr, dev).contiguous()
-    indices = _int32("kv_page_indices", kv_page_indices, dev).contiguous()
-    B, Hq, D = q.shape[0], q.shape[1], q.shape[-1]
-    q4 = q if q.dim() == 4 else q.unsqueeze(2)
-    P, _, Hkv, page, Dc = pool.shape
-    if Dc != D:
-        raise ValueError(f"head_dim mismatch: q has {D}, cache has {Dc}")
-    if indptr.numel() != B + 1:
-        raise ValueError("kv_page_indptr must have B+1 entries")
-    ind, nnz, ist, nst = _sparse_meta(sparse_ind, sparse_nnz, dev, B, Hq)
-    L = ind.shape[2]
-    o = torch.empty((B, Hq, D), dtype=q.dtype, device=dev)
-    lse = torch.empty((B, Hq), dtype=torch.float32, device=dev) if return_lse else None
-    lib = N.load()
-    ws_n = lib.akt_sparse_decode_workspace_size(B, Hq, D, L, num_splits)
-    st = N.stream_of(q)
-    ws = N.workspace(ws_n, dev, st)
-    if lsh_k is None:
-        scale = float(1.0 / math.sqrt(D)) if softmax_scale is None else float(softmax_scale)
-        rc = lib.akt_sparse_decode_paged_fwd(N.ptr(q4), N.ptr(pool), N.ptr(indptr), N.ptr(indices),
-                                             N.ptr(ind), N.ptr(nnz), N.ptr(o), N.ptr(lse), B, Hq,
-                                             Hkv, D, page, P, L, N.strides(q4), N.strides(pool),
-                                             ist, nst, scale, num_splits, N.ptr(ws), ws_n,
-                                             st)
-        N.check(rc, "akt_sparse_decode_paged_fwd")
-    else:
-        for name, t in (("K", lsh_k), ("L", lsh_l)):
-            _need_gpu(name, t)
-            if t.dtype != torch.float32 or tuple(t.shape) != (B, Hq):
-                raise ValueError(f"MagicPIG {name} must be float32 [{B}, {Hq}]")
-        lk, ll = lsh_k.contiguous(), lsh_l.contiguous()
-        rc = lib.akt_magicpig_decode_paged_fwd(N.ptr(q4), N.ptr(pool), N.ptr(indptr),
-                                               N.ptr(indices), N.ptr(ind), N.ptr(nnz), N.ptr(lk),
-                                               N.ptr(ll), N.ptr(o), N.ptr(lse), B, Hq, Hkv, D,
-                                               page, P, L, N.strides(q4), N.strides(pool), ist,
-                                               nst, num_splits, N.ptr(ws), ws_n, st)
-        N.check(rc, "akt_magicpig_decode_paged_fwd")
-    return (o, lse) if return_lse else o
+    return _hot("sparse_decode_paged")(q, paged_kv_cache, kv_page_indptr, kv_page_indices,
+                                       sparse_ind, sparse_nnz, softmax_scale=softmax_scale,
+                                       return_lse=return_lse, num_splits=num_splits,
+                                       lsh_k=lsh_k, lsh_l=lsh_l)
 
 
 # --------------------------------------------------------------------------- CSR kept indices

@@ -1,8 +1,9 @@
 """Build recipe for libakt_amd.so (the gfx950 kernel library).
 
 Compiles every ``csrc/*.hip`` for gfx950 with hipcc and links them into
-``attention_kernel_triton_amd/libakt_amd.so`` (in-tree, so the built library
-travels with the source tree).  Run ``python -m attention_kernel_triton_amd.build``.
+``attention_kernel_triton_amd/libakt_amd.so``, and compiles the host layer
+``csrc/torch_ops.cpp`` into the extension module ``_akt_torch`` (both in-tree,
+so the built libraries travel with the source tree).  Run ``python -m attention_kernel_triton_amd.build``.
 """
 from __future__ import annotations
 
@@ -11,6 +12,7 @@ import os
 import shutil
 import subprocess
 import sys
+import sysconfig
 from pathlib import Path
 
 PKG_DIR = Path(__file__).resolve().parent
@@ -58,8 +60,38 @@ def _run(cmd: list[str]) -> None:
         sys.stderr.write(err + "\n")
 
 
+def torch_ext_path() -> Path:
+    return PKG_DIR / ("_akt_torch" + sysconfig.get_config_var("EXT_SUFFIX"))
+
+
+def torch_ext_command(out: Path) -> list[str]:
+    """g++ line of the compiled host layer (csrc/torch_ops.cpp -> _akt_torch).
+
+    Host code only, built against torch's headers and libraries.  It is not
+    linked to libakt_amd.so: the package loads that library with RTLD_GLOBAL
+    first, and the extension's akt_* references resolve against it.
+    """
+    import torch
+    import torch.utils.cpp_extension as ce
+
+    torch_lib = Path(torch.__file__).resolve().parent / "lib"
+    return [
+        "g++", "-O2", "-std=c++17", "-shared", "-fPIC",
+        f"-D_GLIBCXX_USE_CXX11_ABI={int(torch._C._GLIBCXX_USE_CXX11_ABI)}",
+        "-DTORCH_EXTENSION_NAME=_akt_torch", "-DTORCH_API_INCLUDE_EXTENSION_H",
+        "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1",
+        *[f"-I{p}" for p in ce.include_paths("cuda")],
+        f"-I{sysconfig.get_paths()['include']}",
+        str(CSRC / "torch_ops.cpp"),
+        f"-L{torch_lib}", "-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu", "-ltorch_hip",
+        "-ltorch_python", f"-Wl,-rpath,{torch_lib}",
+        "-o", str(out),
+    ]
+
+
 def build(jobs: int | None = None, verbose: bool = False) -> Path:
-    """Compile all kernels and link the shared library; returns its path."""
+    """Compile all kernels and the host layer and link the shared libraries;
+    returns the kernel library's path."""
     BUILD_DIR.mkdir(exist_ok=True)
     sources = sorted(CSRC.glob("*.hip"))
     if not sources:
@@ -71,6 +103,9 @@ def build(jobs: int | None = None, verbose: bool = False) -> Path:
         obj = BUILD_DIR / (src.stem + ".o")
         objs.append(obj)
         cmds.append([cc, *COMMON_FLAGS, "-c", str(src), "-o", str(obj)])
+    ext_out = torch_ext_path()
+    ext_tmp = ext_out.with_name(ext_out.name + ".tmp")
+    cmds.append(torch_ext_command(ext_tmp))
     jobs = jobs or min(len(cmds), os.cpu_count() or 4, 8)
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
         for cmd, _ in zip(cmds, ex.map(_run, cmds)):
@@ -82,6 +117,7 @@ def build(jobs: int | None = None, verbose: bool = False) -> Path:
         print(" ".join(link))
     _run(link)
     os.replace(tmp, LIB_PATH)
+    os.replace(ext_tmp, ext_out)
     return LIB_PATH
 
 

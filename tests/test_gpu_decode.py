@@ -181,7 +181,9 @@ def test_paged_repeated_calls_are_bit_identical(dev):
     for o in outs[1:]:
         assert torch.equal(o, outs[0])
     from attention_kernel_triton_amd import _native
-    for buf in _native._WS_CACHE.values():
+    bufs = _native.workspace_buffers()
+    assert bufs
+    for _, _, buf in bufs:
         assert int(buf[:256].count_nonzero()) == 0
 
 
@@ -198,7 +200,7 @@ def test_paged_on_a_side_stream_matches_the_default_stream(dev):
         key = (torch.device(dev).index or 0, side.cuda_stream)
     torch.cuda.synchronize(dev)
     assert torch.equal(o, ref)
-    assert key in _native._WS_CACHE
+    assert key in [(d, s) for d, s, _ in _native.workspace_buffers()]
     # ctypes reads the null (default) stream back as None
     assert (_native.stream_of(p.q).value or 0) == torch.cuda.current_stream(dev).cuda_stream
 
