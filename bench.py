@@ -7,15 +7,22 @@ Headline metric: paged decode HBM GB/s + prefill TFLOP/s.
              / wall time per step, inputs resident in HBM.
   prefill  : causal GQA prefill (config 0: Q [8,64,1024,64], K/V [8,16,1024,64])
              -- algorithmic FLOPs / wall time per step.
-A step is one call of the drop-in entry point on the synthetic batch.  Each
-leg carries a roofline object for its dominant kernel (split-KV decode kernel,
-prefill kernel): algorithmic bytes (FLOPs) per launch / the kernel's mean
-duration from a HIP event pair that the runtime stamps with the dispatch's own
-start and end (hipExtLaunchKernel on the launch stream), against MI355X's
-published peak (8 TB/s HBM, 2.5 PFLOP/s dense fp16).  `traffic` is the HBM
-bytes per launch from the committed rocprofv3 counter summary in profiles/.  The CPU
-baseline is the repository's CPU restatement of the reference's naive path
-(oracle/, fp32) timed on a bounded sample on this host.
+  legs     : one leg per other hot-path row (configs 1, 2, 4a, 4b, MagicPIG,
+             the LSE merge, the paged-KV append and kept-index selection).
+
+A step is one call of the drop-in entry point on the synthetic batch, and every
+entry point runs exactly one kernel.  Each leg does W untimed warm-up steps,
+then times K steps bracketed by torch.cuda.synchronize(): ms_per_step is the
+wall clock over them, and roofline.kernel_us is the GPU time of the same K
+launches from a HIP event pair recorded on the launch stream around them (so
+kernel_us <= ms_per_step; it includes the sub-microsecond gaps between
+back-to-back launches).  roofline.achieved is algorithmic bytes (FLOPs) per
+step / kernel_us against MI355X's published peak (8 TB/s HBM, 2.5 PFLOP/s
+dense fp16); roofline.traffic is the HBM bytes per launch from the committed
+rocprofv3 counter summary in profiles/, where one exists.  Legs whose working
+set is under twice the 256 MB Infinity Cache rotate over copies of their
+inputs.  cpu_baseline is the repository's CPU restatement of the reference's
+naive path (oracle/, fp32 torch/numpy) timed on a bounded sample on this host.
 
 Usage: python bench.py [--steps K] [--warmup W] [--gpus 1]
 Prints one JSON line.
@@ -30,6 +37,7 @@ import time
 
 HBM_PEAK_GBS = 8000.0
 FP16_PEAK_TFLOPS = 2500.0
+MALL_BYTES = 256 << 20
 PROFILES = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles")
 
 
@@ -73,32 +81,56 @@ def _log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def _time_steps(fn, steps, warmup):
-    """Wall time per step, and mean dominant-kernel time per step.
-
-    The step time comes from a loop with nothing but the steps in it; the
-    kernel time from a second loop of the same steps in which the library
-    launches its dominant kernel with a HIP event pair stamped on the dispatch.
-    """
+# --------------------------------------------------------------------------- timing
+def _time_steps(fns, steps, warmup):
+    """(wall seconds per step, GPU seconds per step) over `steps` calls cycling
+    through fns (one kernel each), after `warmup` untimed calls."""
     import torch
-    from attention_kernel_triton_amd import _native
-    for _ in range(warmup):
-        fn()
+    n = len(fns)
+    for i in range(warmup):
+        fns[i % n]()
     torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
-    for _ in range(steps):
-        fn()
+    e0.record(stream)
+    for i in range(steps):
+        fns[i % n]()
+    e1.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    with _native.kernel_timer() as kt:
-        for _ in range(steps):
-            fn()
-        torch.cuda.synchronize()
-    if kt.launches != steps:
-        raise RuntimeError(f"expected {steps} timed launches, got {kt.launches}")
-    return wall / steps, kt.total_ms / 1e3 / steps
+    gpu = e0.elapsed_time(e1) / 1e3
+    if gpu > wall:  # the events are recorded inside the wall-clock window
+        raise RuntimeError(f"GPU time {gpu} s exceeds the wall time {wall} s of its own steps")
+    return wall / steps, gpu / steps
 
 
+def _leg(name, fns, work, unit, kernel, args, traffic=None, note=""):
+    """Time a leg; work = algorithmic bytes or FLOPs per step."""
+    steps = max(args.steps, len(fns))
+    t_step, t_kern = _time_steps(fns, steps, max(args.warmup, len(fns)))
+    scale = 1e9 if unit == "GB/s" else 1e12
+    bound = "hbm" if unit == "GB/s" else "mfma"
+    peak = HBM_PEAK_GBS if bound == "hbm" else FP16_PEAK_TFLOPS
+    out = {"value": work / t_step / scale, "unit": unit, "ms_per_step": t_step * 1e3,
+           "work_per_step": work, "steps": steps,
+           "roofline": {"bound": bound, "achieved": work / t_kern / scale, "peak": peak,
+                        "unit": unit, "frac": work / t_kern / scale / peak, "traffic": traffic,
+                        "kernel": kernel, "kernel_us": t_kern * 1e6}}
+    if note:
+        out["note"] = note
+    _log(f"{name}: {out['value']:.1f} {unit} per step ({t_step * 1e6:.1f} us), kernel "
+         f"{t_kern * 1e6:.1f} us, frac {out['roofline']['frac']:.3f}")
+    return out
+
+
+def _copies(nbytes_one, floor=1):
+    """Input sets to rotate so that their total exceeds twice the Infinity Cache."""
+    return max(floor, -(-2 * MALL_BYTES // max(1, nbytes_one)))
+
+
+# --------------------------------------------------------------------------- CPU baseline
 def _cpu_threads():
     """The host threads the CPU baseline uses: the OMP_NUM_THREADS share when the
     environment sets one (the GPU boxes do), else every core."""
@@ -117,63 +149,63 @@ def _cpu_model():
     return "unknown CPU"
 
 
-CPU_BUDGET_S = 10.0  # CPU work per baseline: at least 3 runs, then runs until this is spent
-
-
-def _cpu_time(fn, min_reps=3, budget_s=CPU_BUDGET_S):
-    """Median wall time of fn over runs totalling about budget_s (after a warm-up);
-    returns (median seconds, runs, total seconds)."""
+def _cpu_baseline(fn, work, unit, sample, budget_s, args):
+    """Median wall time of fn (the oracle on a bounded sample of the leg's
+    workload, `work` units of it) over runs totalling about budget_s after one
+    warm-up; one run if a single run exceeds 30 s."""
+    if args.no_cpu_baseline:
+        return None
+    import torch
+    torch.set_num_threads(_cpu_threads())
+    t0 = time.perf_counter()
     fn()  # warm-up
-    ts = []
-    while len(ts) < min_reps or sum(ts) < budget_s:
+    first = time.perf_counter() - t0
+    ts = [first] if first > 30.0 else []
+    while not ts or (first <= 30.0 and (len(ts) < 3 or sum(ts) < budget_s)):
         t0 = time.perf_counter()
         fn()
         ts.append(time.perf_counter() - t0)
-    total = sum(ts)
     ts.sort()
-    return ts[len(ts) // 2], len(ts), total
+    t = ts[len(ts) // 2]
+    scale = 1e9 if unit == "GB/s" else 1e12
+    return {"value": work / t / scale, "unit": unit, "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": f"{sample}; median of {len(ts)} runs ({t * 1e3:.1f} ms each, "
+                      f"{sum(ts):.1f} s in all), fp32 on {torch.get_num_threads()} threads of "
+                      f"{_cpu_model()}"}
 
 
+# --------------------------------------------------------------------------- headline legs
 def bench_paged(args):
     import torch
+    from attention_kernel_triton_amd import decode_flash_attention_redundant_var_len_paged as pg
     from attention_kernel_triton_amd import _ops
     from attention_kernel_triton_amd import synthetic as syn
     dev = torch.device("cuda:0")
     _log("generating config 3 (paged decode)")
     cfg = syn.paged_config()
     p = cfg.to(dev)
-    nbytes = cfg.bytes()
-
-    def step():
-        return _ops.decode_paged(p.q, p.pool, p.indptr, p.indices, p.last_len,
-                                 chunk_tokens=args.chunk)
-
+    nbytes = cfg.bytes()  # 472 MB per step: larger than twice the Infinity Cache
+    if args.chunk:
+        fn = lambda: _ops.decode_paged(p.q, p.pool, p.indptr, p.indices, p.last_len,  # noqa: E731
+                                       chunk_tokens=args.chunk)
+    else:
+        fn = lambda: pg.flash_attention_decode_paged(p.q, p.pool, p.indptr, p.indices,  # noqa: E731
+                                                     p.last_len)
     _log("timing paged decode")
-    t_step, t_kern = _time_steps(step, args.steps, args.warmup)
-    out = {
-        "value": nbytes / t_step / 1e9,
-        "ms_per_step": t_step * 1e3,
-        "bytes_per_step": nbytes,
-        "roofline": {"bound": "hbm", "achieved": nbytes / t_kern / 1e9, "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": nbytes / t_kern / 1e9 / HBM_PEAK_GBS,
-                     "traffic": _traffic("split_kernel_paged_decode_config3.md"),
-                     "kernel": "split_kernel<128,4,kModePaged>",
-                     "kernel_us": t_kern * 1e6},
-        "tokens": sum(cfg.lens),
-    }
-    if not args.no_cpu_baseline:
-        from oracle import naive
-        _log("CPU baseline: oracle naive_paged_attention (fp32) on config 3")
-        torch.set_num_threads(_cpu_threads())
-        t, reps, total = _cpu_time(lambda: naive.naive_paged_attention(
-            cfg.q, cfg.pool, cfg.indptr, cfg.indices, cfg.last_len, dtype=torch.float32))
-        out["cpu_baseline"] = {"value": nbytes / t / 1e9, "unit": "GB/s",
-                               "cores": torch.get_num_threads(), "kind": "port",
-                               "sample": f"full config 3 batch, median of {reps} runs "
-                                         f"({t * 1e3:.0f} ms each, {total:.1f} s in all), "
-                                         f"fp32 torch on "
-                                         f"{torch.get_num_threads()} threads of {_cpu_model()}"}
+    out = _leg("config 3", [fn], nbytes, "GB/s", "split_kernel<128,4,kModePaged>", args,
+               traffic=_traffic("split_kernel_paged_decode_config3.md"))
+    out["tokens"] = sum(cfg.lens)
     del p
+
+    def cpu():
+        from oracle import naive
+        naive.naive_paged_attention(cfg.q, cfg.pool, cfg.indptr, cfg.indices, cfg.last_len,
+                                    dtype=torch.float32)
+
+    _log("CPU baseline: oracle naive_paged_attention on config 3")
+    out["cpu_baseline"] = _cpu_baseline(cpu, nbytes, "GB/s", "the full config 3 batch",
+                                        10.0, args)
     return out
 
 
@@ -186,75 +218,26 @@ def bench_prefill(args):
     cfg = syn.prefill_config(0)
     c = cfg.to(dev)
     flops = cfg.flops()
-
-    def step():
-        return pre.flash_attention_prefill(c.Q, c.K, c.V, True, c.scale, c.group)
-
     _log("timing prefill")
-    t_step, t_kern = _time_steps(step, args.steps, args.warmup)
-    out = {
-        "value": flops / t_step / 1e12,
-        "unit": "TFLOP/s",
-        "ms_per_step": t_step * 1e3,
-        "flops_per_step": flops,
-        "roofline": {"bound": "mfma", "achieved": flops / t_kern / 1e12, "peak": FP16_PEAK_TFLOPS,
-                     "unit": "TFLOP/s", "frac": flops / t_kern / 1e12 / FP16_PEAK_TFLOPS,
-                     "traffic": _traffic("prefill_kernel_causal_config0.md"),
-                     "kernel": "prefill_kernel<64,causal>",
-                     "kernel_us": t_kern * 1e6},
-    }
-    if not args.no_cpu_baseline:
+    out = _leg("config 0", [lambda: pre.flash_attention_prefill(c.Q, c.K, c.V, True, c.scale,
+                                                                c.group)],
+               flops, "TFLOP/s", "prefill_kernel<64,causal>", args,
+               traffic=_traffic("prefill_kernel_causal_config0.md"))
+    del c
+    nb = 2
+
+    def cpu():
         from oracle import naive
-        _log("CPU baseline: oracle prefill (fp32) on 2 of 8 batches of config 0")
-        torch.set_num_threads(_cpu_threads())
-        nb = 2
-        t, reps, total = _cpu_time(lambda: naive.prefill(
-            cfg.Q[:nb], cfg.K[:nb], cfg.V[:nb], True, cfg.scale, cfg.group, dtype=torch.float32))
-        out["cpu_baseline"] = {"value": flops * nb / 8 / t / 1e12, "unit": "TFLOP/s",
-                               "cores": torch.get_num_threads(), "kind": "port",
-                               "sample": f"2 of 8 batches of config 0, median of {reps} runs "
-                                         f"({t * 1e3:.0f} ms each, {total:.1f} s in all), "
-                                         f"fp32 torch on "
-                                         f"{torch.get_num_threads()} threads of {_cpu_model()}"}
+        naive.prefill(cfg.Q[:nb], cfg.K[:nb], cfg.V[:nb], True, cfg.scale, cfg.group,
+                      dtype=torch.float32)
+
+    _log("CPU baseline: oracle prefill on 2 of 8 batches of config 0")
+    out["cpu_baseline"] = _cpu_baseline(cpu, flops * nb // 8, "TFLOP/s",
+                                        "2 of the 8 batches of config 0", 10.0, args)
     return out
 
 
 # --------------------------------------------------------------------------- other rows
-# Secondary legs: one per remaining hot-path row, each with the roofline of its
-# dominant kernel.  Inputs are rotated over several copies (or kept-index sets)
-# whose total exceeds the 256 MB Infinity Cache, so HBM-bound legs are not
-# measured out of the cache.
-MALL_BYTES = 256 << 20
-
-
-def _copies(nbytes_one, floor=2):
-    return max(floor, -(-2 * MALL_BYTES // max(1, nbytes_one)))
-
-
-def _leg(name, fn_list, work, unit, bound, kernel, args, note=""):
-    """Time a leg that cycles through fn_list; work = algorithmic bytes or FLOPs per step."""
-    i = [0]
-
-    def step():
-        fn_list[i[0] % len(fn_list)]()
-        i[0] += 1
-
-    steps = max(args.steps, len(fn_list))
-    t_step, t_kern = _time_steps(step, steps, max(args.warmup, len(fn_list)))
-    scale = 1e9 if unit == "GB/s" else 1e12
-    peak = HBM_PEAK_GBS if bound == "hbm" else FP16_PEAK_TFLOPS
-    out = {"value": work / t_step / scale, "unit": unit, "ms_per_step": t_step * 1e3,
-           "work_per_step": work,
-           "roofline": {"bound": bound, "achieved": work / t_kern / scale, "peak": peak,
-                        "unit": unit, "frac": work / t_kern / scale / peak, "traffic": None,
-                        "kernel": kernel, "kernel_us": t_kern * 1e6}}
-    if note:
-        out["note"] = note
-    _log(f"{name}: {out['value']:.1f} {unit} (kernel {t_kern * 1e6:.1f} us, "
-         f"frac {out['roofline']['frac']:.3f})")
-    return out
-
-
 def _sparse_bytes(ind, nnz, group, D, qo_rows):
     """Unique K/V rows per (batch, kv head) x 4D bytes + indices + q/o/lse."""
     import torch
@@ -272,111 +255,213 @@ def bench_legs(args):
     from attention_kernel_triton_amd import _ops, kept_index
     from attention_kernel_triton_amd import synthetic as syn
     from attention_kernel_triton_amd.paged_kv import append_paged_kv
-    from oracle.kept import kept_from_uniform
     dev = torch.device("cuda:0")
     legs = {}
+    budget = 4.0
 
+    # ---- config 1: var-len causal prefill (compute-bound: no rotation)
     _log("leg: var-len causal prefill, config 1")
     c1 = syn.prefill_config(1)
     d1 = c1.to(dev)
     legs["prefill_varlen_config1"] = _leg(
         "config 1", [lambda: _ops.prefill(d1.Q, d1.K, d1.V, True, d1.scale, varlen=d1.varlen)],
-        c1.flops(), "TFLOP/s", "mfma", "prefill_kernel<64,causal,varlen>", args,
-        "FLOPs over each sequence's valid causal pairs")
+        c1.flops(), "TFLOP/s", "prefill_kernel<64,causal,varlen>", args,
+        note="FLOPs over each sequence's valid causal pairs")
     del d1
     torch.cuda.empty_cache()
+    lens1 = [int(x) for x in c1.varlen.tolist()]
 
+    def cpu1():
+        from oracle import naive
+        naive.prefill_varlen(c1.Q[:2], c1.K[:2], c1.V[:2], True, c1.scale, c1.group,
+                             c1.varlen[:2], dtype=torch.float32)
+
+    fl1 = 4 * 64 * 64 * sum(L * (L + 1) // 2 for L in lens1[:2])
+    legs["prefill_varlen_config1"]["cpu_baseline"] = _cpu_baseline(
+        cpu1, fl1, "TFLOP/s", f"the first 2 of 8 sequences of config 1 (lengths {lens1[:2]})",
+        budget, args)
+
+    # ---- config 2: dense GQA decode (33.7 MB: rotated)
     _log("leg: dense GQA decode, config 2")
     c2 = syn.decode_config()
     n2 = _copies(c2.bytes())
     d2 = [c2.to(dev) for _ in range(n2)]
     legs["decode_config2"] = _leg(
         "config 2", [lambda d=d: _ops.decode(d.q, d.K, d.V, d.scale) for d in d2], c2.bytes(),
-        "GB/s", "hbm", "split_kernel<64,4,kModeDense>", args,
-        f"inputs rotated over {n2} copies")
+        "GB/s", "split_kernel<64,4,kModeDense>", args, note=f"inputs rotated over {n2} copies")
     del d2
     torch.cuda.empty_cache()
 
+    def cpu2():
+        from oracle import naive
+        naive.decode(c2.q, c2.K, c2.V, c2.scale, c2.group, dtype=torch.float32)
+
+    legs["decode_config2"]["cpu_baseline"] = _cpu_baseline(
+        cpu2, c2.bytes(), "GB/s", "the full config 2 batch", budget, args)
+
+    # ---- config 4a: sparse-token decode + LSE (K/V rotated)
     _log("leg: sparse-token decode, config 4a")
     s4 = syn.sparse_config()
     B, H, N = s4.uniform.shape
-    ind, nnz = kept_from_uniform(s4.uniform.reshape(B * H, N).numpy(), s4.kept_ratio, s4.l_max,
-                                 s4.row_len.reshape(-1).numpy())
-    ind = torch.from_numpy(ind).reshape(B, H, -1)
-    nnz = torch.from_numpy(nnz).reshape(B, H, 1)
-    b4 = _sparse_bytes(ind, nnz, s4.group, 128, B * H)
-    n4 = _copies(s4.K.numel() * 4)
+    ind4, nnz4 = kept_index.select_kept(s4.l_max, uniform=s4.uniform.to(dev),
+                                        kept_ratio=s4.kept_ratio, row_len=s4.row_len.to(dev))
+    ind4c, nnz4c = ind4.cpu(), nnz4.cpu()
+    b4 = _sparse_bytes(ind4c, nnz4c, s4.group, 128, B * H)
+    n4 = _copies((s4.K.numel() + s4.V.numel()) * 2)
     kv4 = [(s4.K.to(dev), s4.V.to(dev)) for _ in range(n4)]
-    q4, i4, z4 = s4.q.to(dev), ind.to(dev), nnz.to(dev)
+    q4 = s4.q.to(dev)
     legs["sparse_config4a"] = _leg(
-        "config 4a", [lambda kv=kv: _ops.sparse_decode(q4, kv[0], kv[1], i4, z4, s4.scale,
+        "config 4a", [lambda kv=kv: _ops.sparse_decode(q4, kv[0], kv[1], ind4, nnz4, s4.scale,
                                                       return_lse=True) for kv in kv4],
-        b4, "GB/s", "hbm", "split_kernel<128,1,kModeSparseDense>", args,
-        f"O + LSE; K/V rotated over {n4} copies; bytes = unique kept rows per kv head")
+        b4, "GB/s", "split_kernel<128,1,kModeSparseDense>", args,
+        note=f"O + LSE; K/V rotated over {n4} copies; bytes = unique kept rows per kv head")
     del kv4
     torch.cuda.empty_cache()
 
+    def cpu4():
+        from oracle import naive
+        naive.sparsetoken_naive_decode(s4.q, s4.K, s4.V, ind4c, nnz4c, s4.scale, s4.group,
+                                       dtype=torch.float32)
+
+    legs["sparse_config4a"]["cpu_baseline"] = _cpu_baseline(
+        cpu4, b4, "GB/s", "the full config 4a batch", budget, args)
+
+    # ---- config 4b: sparse paged + MagicPIG decode (kept-index sets rotated)
     _log("leg: sparse paged + MagicPIG decode, config 4b")
     s5 = syn.sparse_paged_config()
     p5 = s5.paged.to(dev)
     B, H, N = s5.uniform.shape
     sets = []
-    nsets = 0
     b5 = 0
     gen = torch.Generator(device=dev).manual_seed(7)
     while True:  # distinct kept-index sets until their gathered rows exceed 2x the cache
         u = torch.rand((B, H, N), generator=gen, device=dev)
-        ind5, nnz5 = kept_index.select_kept(s5.l_max, uniform=u, kept_ratio=s5.kept_ratio,
-                                            row_len=s5.row_len.to(dev))
-        sets.append((ind5, nnz5))
-        nsets += 1
-        if nsets == 1:
-            b5 = _sparse_bytes(ind5.cpu(), nnz5.cpu(), s5.group, 256, B * H) + \
+        sets.append(kept_index.select_kept(s5.l_max, uniform=u, kept_ratio=s5.kept_ratio,
+                                           row_len=s5.row_len.to(dev)))
+        if len(sets) == 1:
+            b5 = _sparse_bytes(sets[0][0].cpu(), sets[0][1].cpu(), s5.group, 256, B * H) + \
                 4 * (p5.indices.numel() + p5.indptr.numel())
-        if nsets * b5 >= 2 * MALL_BYTES or nsets >= 64:
+        if len(sets) * b5 >= 2 * MALL_BYTES or len(sets) >= 64:
             break
     legs["sparse_paged_config4b"] = _leg(
         "config 4b", [lambda st=st: _ops.sparse_decode_paged(p5.q, p5.pool, p5.indptr, p5.indices,
                                                              st[0], st[1], return_lse=True)
                       for st in sets],
-        b5, "GB/s", "hbm", "split_kernel<256,1,kModeSparsePaged>", args,
-        f"O + LSE; {nsets} kept-index sets rotated")
+        b5, "GB/s", "split_kernel<256,1,kModeSparsePaged>", args,
+        note=f"O + LSE; {len(sets)} kept-index sets rotated")
     lk, ll = s5.lsh_k.to(dev), s5.lsh_l.to(dev)
     legs["magicpig_config4b"] = _leg(
         "config 4b MagicPIG", [lambda st=st: _ops.sparse_decode_paged(
             p5.q, p5.pool, p5.indptr, p5.indices, st[0], st[1], return_lse=True, lsh_k=lk,
             lsh_l=ll) for st in sets],
-        b5, "GB/s", "hbm", "split_kernel<256,1,kModeSparsePaged,magicpig>", args,
-        f"O + LSE with norm; {nsets} kept-index sets rotated")
+        b5, "GB/s", "split_kernel<256,1,kModeSparsePaged,magicpig>", args,
+        note=f"O + LSE with norm; {len(sets)} kept-index sets rotated")
+    ind5, nnz5 = sets[0][0].cpu(), sets[0][1].cpu()
     del p5, sets
     torch.cuda.empty_cache()
+    pc = s5.paged
 
+    def cpu5():
+        from oracle import naive
+        naive.sparsetoken_naive_paged_attention(pc.q, pc.pool, pc.indptr, pc.indices, ind5, nnz5,
+                                                dtype=torch.float32)
+
+    def cpu6():
+        from oracle import naive
+        naive.magicpig_sparsetoken_naive_paged_attention(pc.q, pc.pool, pc.indptr, pc.indices,
+                                                         ind5, nnz5, s5.lsh_k, s5.lsh_l,
+                                                         dtype=torch.float32)
+
+    legs["sparse_paged_config4b"]["cpu_baseline"] = _cpu_baseline(
+        cpu5, b5, "GB/s", "the full config 4b batch (first kept-index set)", budget, args)
+    legs["magicpig_config4b"]["cpu_baseline"] = _cpu_baseline(
+        cpu6, b5, "GB/s", "the full config 4b batch (first kept-index set)", budget, args)
+
+    # ---- kept-index selection over config 4b's keep draws (sets rotated)
+    _log("leg: kept-index selection, config 4b draws")
+    rl = s5.row_len.to(dev)
+    lens5 = [int(x) for x in s5.row_len.reshape(-1).tolist()]
+    bk = 4 * sum(lens5) + 4 * B * H * s5.l_max + 4 * B * H
+    nk = _copies(bk + 4 * B * H * N)
+    draws = [torch.rand((B, H, N), generator=gen, device=dev) for _ in range(nk)]
+    legs["kept_index_config4b"] = _leg(
+        "kept index", [lambda u=u: kept_index.select_kept(s5.l_max, uniform=u,
+                                                          kept_ratio=s5.kept_ratio, row_len=rl)
+                       for u in draws],
+        bk, "GB/s", "kept_index_kernel", args,
+        note=f"{B * H} rows of up to {N} fp32 draws; {nk} draw sets rotated; bytes = draws "
+             f"read + padded index rows and counts written")
+    del draws
+    torch.cuda.empty_cache()
+    u5 = s5.uniform.reshape(B * H, N).numpy()
+    rl5 = s5.row_len.reshape(-1).numpy()
+
+    def cpu7():
+        from oracle.kept import kept_from_uniform
+        kept_from_uniform(u5, s5.kept_ratio, s5.l_max, rl5)
+
+    legs["kept_index_config4b"]["cpu_baseline"] = _cpu_baseline(
+        cpu7, bk, "GB/s", "all 96 rows of config 4b's draws (numpy)", budget, args)
+
+    # ---- LSE merge of two fp16 partial states over config 0's rows (rotated)
     _log("leg: LSE merge of partial states")
     rows, D, parts = 8 * 64 * 1024, 64, 2
-    mo = torch.randn(parts, rows, D, device=dev).half()
-    ml = torch.randn(parts, rows, device=dev)
     mb = parts * rows * (D * 2 + 4) + rows * (D * 2 + 4)
+    nm = _copies(mb)
+    mins = [(torch.randn(parts, rows, D, device=dev).half(), torch.randn(parts, rows, device=dev))
+            for _ in range(nm)]
     legs["merge_states"] = _leg(
-        "merge", [lambda: _ops.merge_states(mo, ml)], mb, "GB/s", "hbm", "merge_kernel<f16,f16>",
-        args, f"{parts} fp16 parts of [{rows}, {D}] (config 0's rows) -> fp16")
-    del mo, ml
+        "merge", [lambda m=m: _ops.merge_states(m[0], m[1]) for m in mins], mb, "GB/s",
+        "merge_kernel<f16,f16>", args,
+        note=f"{parts} fp16 parts of [{rows}, {D}] (config 0's rows) -> fp16; {nm} input sets "
+             f"rotated")
+    mo_c, ml_c = mins[0][0][:, : rows // 16].cpu(), mins[0][1][:, : rows // 16].cpu()
+    del mins
     torch.cuda.empty_cache()
 
+    def cpu8():
+        from oracle import naive
+        naive.merge_states(mo_c, ml_c, dtype=torch.float32)
+
+    legs["merge_states"]["cpu_baseline"] = _cpu_baseline(
+        cpu8, mb // 16, "GB/s", "1/16 of the rows", budget, args)
+
+    # ---- paged KV append: 32 sequences x 1024 tokens into random pages (rotated)
     _log("leg: paged KV append (prefill-sized)")
     Bq, Hkv, D, page, T = 32, 8, 128, 16, 1024
     pages = Bq * T // page
-    pool = torch.zeros((pages, 2, Hkv, page, D), dtype=torch.float16, device=dev)
     perm = torch.randperm(pages, generator=torch.Generator().manual_seed(3)).to(torch.int32)
     indptr = torch.arange(0, pages + 1, T // page, dtype=torch.int32)
     last = torch.full((Bq,), page, dtype=torch.int32)
     ap = torch.arange(0, Bq * T + 1, T, dtype=torch.int32)
-    kn = torch.randn(Bq * T, Hkv, D, device=dev).half()
-    vn = torch.randn(Bq * T, Hkv, D, device=dev).half()
     t_dev = [x.to(dev) for x in (ap, indptr, perm, last)]
+    ab = 8 * Bq * T * Hkv * D + 4 * (pages + 2 * Bq + 2)
+    na = _copies(ab)
+    asets = [(torch.randn(Bq * T, Hkv, D, device=dev).half(),
+              torch.randn(Bq * T, Hkv, D, device=dev).half(),
+              torch.zeros((pages, 2, Hkv, page, D), dtype=torch.float16, device=dev))
+             for _ in range(na)]
     legs["paged_append"] = _leg(
-        "append", [lambda: append_paged_kv(kn, vn, t_dev[0], pool, t_dev[1], t_dev[2], t_dev[3])],
-        8 * Bq * T * Hkv * D + 4 * (pages + 2 * Bq + 2), "GB/s", "hbm", "paged_append_kernel",
-        args, f"{Bq} sequences x {T} tokens into random pages")
+        "append", [lambda a=a: append_paged_kv(a[0], a[1], t_dev[0], a[2], t_dev[1], t_dev[2],
+                                               t_dev[3]) for a in asets],
+        ab, "GB/s", "paged_append_kernel", args,
+        note=f"{Bq} sequences x {T} tokens into random pages; {na} input sets rotated; bytes = "
+             f"new K/V rows read and written once")
+    nb_cpu = 2
+    kn_c = asets[0][0][: nb_cpu * T].cpu().numpy()
+    vn_c = asets[0][1][: nb_cpu * T].cpu().numpy()
+    del asets
+    torch.cuda.empty_cache()
+    pool_c = torch.zeros((pages, 2, Hkv, page, D), dtype=torch.float16).numpy()
+
+    def cpu9():
+        from oracle.kept import paged_append
+        paged_append(pool_c, kn_c, vn_c, ap[: nb_cpu + 1].numpy(),
+                     indptr[: nb_cpu + 1].numpy(), perm.numpy(), last[:nb_cpu].numpy())
+
+    legs["paged_append"]["cpu_baseline"] = _cpu_baseline(
+        cpu9, 8 * nb_cpu * T * Hkv * D, "GB/s",
+        f"{nb_cpu} of the {Bq} sequences (numpy, one token at a time)", budget, args)
     return legs
 
 
@@ -404,10 +489,11 @@ def main():
         sys.exit(1)
     from attention_kernel_triton_amd import _native
     _native.load()
+    _native.torch_ext()
     res = {"metric": "paged decode HBM GB/s + prefill TFLOP/s (fp16, % MI355X peak), 1 GPU",
            "value": None, "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
            "warmup": args.warmup, "ms_per_step": None, "higher_is_better": True,
-           "scaling": "weak", "vs_baseline": None, "dtype": "fp16 (fp32 accumulate)",
+           "scaling": "weak", "vs_baseline": None, "dtype": "fp16",
            "data": "synthetic (seeded N(0,1) fp16)",
            "config": {"workload": "paged var-len GQA decode, config 3", "batch": 32,
                       "num_q_heads": 32, "num_kv_heads": 8, "head_dim": 128, "page_size": 16,
@@ -417,9 +503,11 @@ def main():
         res["value"] = pg.pop("value")
         res["ms_per_step"] = pg.pop("ms_per_step")
         res["roofline"] = pg.pop("roofline")
-        if "cpu_baseline" in pg:
-            res["cpu_baseline"] = pg.pop("cpu_baseline")
-        res["config"].update(pg)
+        cb = pg.pop("cpu_baseline", None)
+        if cb:
+            res["cpu_baseline"] = cb
+        pg.pop("unit", None)
+        res["config"].update({"bytes_per_step": pg.pop("work_per_step"), "tokens": pg["tokens"]})
         torch.cuda.empty_cache()
     if args.only in ("all", "headline", "prefill"):
         pf = bench_prefill(args)
@@ -429,6 +517,7 @@ def main():
         if res["value"] is None:
             res.update({"value": pf["value"], "unit": pf["unit"],
                         "ms_per_step": pf["ms_per_step"], "roofline": pf["roofline"]})
+        torch.cuda.empty_cache()
     if args.only in ("all", "legs"):
         res["legs"] = bench_legs(args)
     if args.copy_calibration_mb:

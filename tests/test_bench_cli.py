@@ -17,7 +17,7 @@ def test_more_than_one_gpu_is_refused_with_a_message():
     assert "one GPU" in msg["error"]
 
 
-def test_cpu_baseline_timer_spends_its_budget_and_takes_the_median():
+def test_cpu_baseline_spends_its_budget_and_takes_the_median():
     import bench
     durations = iter([0.03, 0.01, 0.02] + [0.01] * 100)
     calls = []
@@ -26,7 +26,13 @@ def test_cpu_baseline_timer_spends_its_budget_and_takes_the_median():
         calls.append(1)
         time.sleep(next(durations))
 
-    t, runs, total = bench._cpu_time(fn, min_reps=3, budget_s=0.05)
-    assert runs >= 3 and total >= 0.05
-    assert len(calls) == runs + 1  # one warm-up call
-    assert 0.009 < t < 0.03
+    class Args:
+        no_cpu_baseline = False
+
+    r = bench._cpu_baseline(fn, 1e9, "GB/s", "a sample", 0.05, Args)
+    runs = int(r["sample"].split("median of ")[1].split()[0])
+    assert runs >= 3 and len(calls) == runs + 1  # one warm-up call
+    assert r["kind"] == "port" and r["cores"] >= 1 and r["unit"] == "GB/s"
+    assert 1 / 0.03 < r["value"] < 1 / 0.009  # 1 GB over the median run of 10-20 ms
+    Args.no_cpu_baseline = True
+    assert bench._cpu_baseline(fn, 1e9, "GB/s", "a sample", 0.05, Args) is None
