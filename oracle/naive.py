@@ -192,7 +192,7 @@ def sparsetoken_naive_paged_attention(q, paged_kv_cache, kv_page_indptr, kv_page
     Returns (O [B, Hq, D], lse [B, Hq]).
     """
     B, Hq, D = q.shape[0], q.shape[1], q.shape[-1]
-    pool = _cpu(paged_kv_cache, dtype)
+    pool = paged_kv_cache.detach().cpu()  # rows are converted to `dtype` once gathered
     Hkv, page = pool.shape[2], pool.shape[3]
     G = Hq // Hkv
     scale = 1.0 / math.sqrt(D) if softmax_scale is None else softmax_scale
@@ -209,8 +209,8 @@ def sparsetoken_naive_paged_attention(q, paged_kv_cache, kv_page_indptr, kv_page
             if n == 0:
                 continue
             t = ind[b, h, :n]
-            k = _paged_rows(pool, indptr[b], indices, t, page, h // G, 0)
-            v = _paged_rows(pool, indptr[b], indices, t, page, h // G, 1)
+            k = _paged_rows(pool, indptr[b], indices, t, page, h // G, 0).to(dtype)
+            v = _paged_rows(pool, indptr[b], indices, t, page, h // G, 1).to(dtype)
             out[b, h], lse[b, h] = _attend(qc[b, h], k, v, scale)
     return out, lse
 
@@ -244,7 +244,7 @@ def magicpig_sparsetoken_naive_paged_attention(q, paged_kv_cache, kv_page_indptr
     Returns (O [B, Hq, D], lse [B, Hq]) with lse = ln sum_i exp(score_i).
     """
     B, Hq, D = q.shape[0], q.shape[1], q.shape[-1]
-    pool = _cpu(paged_kv_cache, dtype)
+    pool = paged_kv_cache.detach().cpu()  # rows are converted to `dtype` once gathered
     Hkv, page = pool.shape[2], pool.shape[3]
     G = Hq // Hkv
     qc = _cpu(q, dtype).reshape(B, Hq, D)
@@ -261,8 +261,8 @@ def magicpig_sparsetoken_naive_paged_attention(q, paged_kv_cache, kv_page_indptr
             if n == 0:
                 continue
             t = ind[b, h, :n]
-            k = _paged_rows(pool, indptr[b], indices, t, page, h // G, 0)
-            v = _paged_rows(pool, indptr[b], indices, t, page, h // G, 1)
+            k = _paged_rows(pool, indptr[b], indices, t, page, h // G, 0).to(dtype)
+            v = _paged_rows(pool, indptr[b], indices, t, page, h // G, 1).to(dtype)
             sc = magicpig_scores(qc[b, h], k, Kc[b, h], Lc[b, h], D, dtype)
             lse[b, h] = torch.logsumexp(sc, dim=0)
             out[b, h] = torch.matmul(torch.softmax(sc, dim=0), v)

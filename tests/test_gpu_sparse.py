@@ -262,3 +262,52 @@ def test_sparse_splits_merge_deterministically(dev):
     for _ in range(5):
         o, lse = sp.sparsetoken_flash_attention_decode(*args, return_lse=True)
         assert torch.equal(o, o0) and torch.equal(lse, l0)
+
+
+def _reference_harness_fixture(dev):
+    """The reference harness's sparse paged / MagicPIG case at its own shape
+    (sparsetoken_decode_flash_attention_redundant_var_len_paged.py:296-330,
+    magicpig_..._with_norm.py:296-317): a 1024-page pool of page size 256 and
+    head dim 256, 8 kv heads and 32 query heads, three sequences of 270 / 350 /
+    321 pages over a random permutation of the first 941 page ids with last
+    page lengths 63 / 22 / 55, kept ratio 0.02 over each sequence's tokens,
+    L_max = 512 * 256 index slots, MagicPIG K, L ~ U[1, 6)."""
+    g = torch.Generator(device=dev).manual_seed(61)
+    gc = torch.Generator().manual_seed(62)
+    B, Hkv, G, D, page = 3, 8, 4, 256, 256
+    Hq = Hkv * G
+    pool = torch.randn(1024, 2, Hkv, page, D, generator=g, device=dev, dtype=torch.float16)
+    npg = torch.tensor([270, 350, 321], dtype=torch.int32)
+    indices = torch.randperm(int(npg.sum()), generator=gc).to(torch.int32)
+    indptr = torch.zeros(B + 1, dtype=torch.int32)
+    indptr[1:] = torch.cumsum(npg, 0)
+    last = torch.tensor([63, 22, 55], dtype=torch.int32)
+    lens = (npg - 1) * page + last
+    l_max = 512 * page
+    u = torch.rand((B, Hq, l_max), generator=g, device=dev)
+    row_len = lens.view(B, 1).expand(B, Hq).contiguous().to(dev)
+    ind, nnz = kept_index.select_kept(l_max, uniform=u, kept_ratio=0.02, row_len=row_len)
+    q = torch.randn(B, Hq, 1, D, generator=g, device=dev, dtype=torch.float16)
+    K = torch.rand(B, Hq, generator=gc) * 5 + 1
+    L = torch.rand(B, Hq, generator=gc) * 5 + 1
+    return q, pool, indptr, indices, ind, nnz, K, L
+
+
+def test_sparse_paged_and_magicpig_on_the_reference_harness_fixture(dev):
+    q, pool, indptr, indices, ind, nnz, K, L = _reference_harness_fixture(dev)
+    o, lse = spp.sparsetoken_flash_attention_decode_paged(q, pool, indptr.to(dev),
+                                                          indices.to(dev), ind, nnz,
+                                                          return_lse=True)
+    mo, ml = mp.magicpig_sparsetoken_flash_attention_decode_paged(
+        q, pool, indptr.to(dev), indices.to(dev), ind, nnz, K.to(dev), L.to(dev),
+        return_lse=True)
+    qc, pc, ic, zc = q.cpu(), pool.cpu(), ind.cpu(), nnz.cpu()
+    ro, rl = naive.sparsetoken_naive_paged_attention(qc, pc, indptr, indices, ic, zc)
+    err = assert_close(o, ro, what="harness fixture, sparse paged")
+    assert_close(lse, rl, atol=1e-4, what="harness fixture, sparse paged lse")
+    r64, l64 = naive.magicpig_sparsetoken_naive_paged_attention(qc, pc, indptr, indices, ic, zc,
+                                                                 K, L)
+    merr = assert_close(mo, r64, what="harness fixture, MagicPIG vs fp64 oracle")
+    assert_close(ml, l64, atol=1e-3, what="harness fixture, MagicPIG lse vs fp64 oracle")
+    print(f"harness fixture: sparse paged err {err:.3e}, MagicPIG err {merr:.3e}, "
+          f"kept per head {float(zc.float().mean()):.0f}")
