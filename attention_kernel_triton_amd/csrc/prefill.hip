@@ -47,10 +47,8 @@
 // stays below 32 * 2^kRescaleSlack and the O rescale is almost never run.  P
 // is rounded to fp16 for P.V (as the reference does at
 // prefill_flash_attention.py:94) and the normaliser sums the same rounded
-// values, on the matrix pipe (see softmax below).  That sum pairs row n with
-// row n + 16 through zero weights, so a query row holding NaN also turns its
-// partner row's output to NaN; finite inputs are unaffected, and var-len
-// padding rows are read as zeros.
+// values, each row on its own (a NaN query row leaves every other row
+// exact, as in the reference).
 //
 // Masking uses a select (score = -inf), not the reference's additive -1e6
 // (prefill_flash_attention.py:76), so non-finite padding never leaks.  In
@@ -68,9 +66,13 @@ namespace {
 
 constexpr int kPThreads = 256;
 constexpr int kSlots = 4;   // waves per workgroup
-constexpr int kRows = 64;   // query rows per slot (two 32-row MFMA blocks)
-constexpr int kBN = 64;     // keys per staged tile
 constexpr int kNBuf = 4;    // LDS tile buffers
+// 32-row MFMA blocks per wave, query rows per slot and keys per staged tile:
+// two blocks and 64-key tiles up to D = 128; at D = 192 and 256 one block (the
+// register budget) and 32-key tiles (four K + V buffers then fit in 128 KB).
+__host__ __device__ constexpr int rblocks_for(int D) { return D >= 192 ? 1 : 2; }
+__host__ __device__ constexpr int rows_for(int D) { return 32 * rblocks_for(D); }
+__host__ __device__ constexpr int tile_keys_for(int D) { return D >= 192 ? 32 : 64; }
 constexpr float kRescaleSlack = 8.0f;
 // Largest row sum of one 32-key step that lets P stay unchecked: below it
 // every probability is under 32 * 2^kRescaleSlack, far inside fp16's range;
@@ -93,7 +95,7 @@ struct PrefillParams {
   int64_t o_sb, o_sh, o_ss;
   int B, Hq, Hkv, G, S;
   int varlen_bits;
-  int n_rb;      // 64-row blocks per sequence
+  int n_rb;      // query row blocks (slots of one head) per sequence
   int n_sg;      // slot groups (workgroups) per (batch, kv head)
   int grid1d;    // 1: linear grid (a dimension past 65535); 0: grid (Hkv, B, n_sg)
   int fast_div;  // 1: G * n_rb + kSlots < 2^22, slot / G through g_inv
@@ -157,6 +159,10 @@ __device__ __forceinline__ int div_small(int n, int d, float inv) {
 template <int D, bool CAUSAL, bool VARLEN>
 __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(D == 64 ? 2 : 1, 2)))
 void prefill_kernel(PrefillParams p) {
+  constexpr int NRB = rblocks_for(D);     // 32-row MFMA blocks per wave
+  constexpr int kRows = rows_for(D);      // query rows per slot
+  constexpr int kBN = tile_keys_for(D);   // keys per staged tile
+  constexpr int SPT = kBN / 32;           // 32-key steps per tile
   constexpr int KS = D / 16;              // MFMA k-steps over the head dim
   constexpr int HALF = D / 2;             // head dims per lane half in S^T operands
   constexpr int NT = D / 32;              // 32-dim output tiles
@@ -212,7 +218,9 @@ void prefill_kernel(PrefillParams p) {
     kv_end = min(row_lim, div_g(f_last) * kRows + kRows);
   }
   const int key_lim = (VARLEN && CAUSAL) ? len : S;  // rows at or past this are never staged
-  const int n_tiles = uniform((kv_end + kBN - 1) / kBN);
+  // Tiles staged by the workgroup; with one step per tile, rounded up to a
+  // pair of steps (the pair's padding tile past the keys reads as zeros).
+  const int n_tiles = uniform(SPT == 2 ? (kv_end + kBN - 1) / kBN : 2 * ((kv_end + 63) / 64));
   if (n_tiles == 0) return;
   const int wave_kv_end = CAUSAL ? min(kv_end, r0 + kRows) : kv_end;
   // 32-key steps of this wave, rounded up to a pair.  A padding step covers
@@ -243,12 +251,16 @@ void prefill_kernel(PrefillParams p) {
     vvo[i] = (int)(r * p.v_ss * 2) + 16 * cc;
   }
   auto load_tile_to = [&](int j, uint4_t (&kd)[PER_T], uint4_t (&vd)[PER_T]) {
-    const int rows = uniform(min(kBN, key_lim - j * kBN));  // >= 1: tiles start below key_lim
+    // Rows of tile j below key_lim; none for a padding tile (an empty range:
+    // every read returns zeros and no memory is touched).
+    const int rows = uniform(min(kBN, key_lim - j * kBN));
     const int64_t row0 = (int64_t)j * kBN;
-    const auto kr = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(Kh + row0 * p.k_ss), 0, (int)((rows - 1) * p.k_ss * 2) + ROWB, kBufferWord3);
-    const auto vr = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(Vh + row0 * p.v_ss), 0, (int)((rows - 1) * p.v_ss * 2) + ROWB, kBufferWord3);
+    const int kbytes = rows > 0 ? (int)((rows - 1) * p.k_ss * 2) + ROWB : 0;
+    const int vbytes = rows > 0 ? (int)((rows - 1) * p.v_ss * 2) + ROWB : 0;
+    const auto kr = __builtin_amdgcn_make_buffer_rsrc((void*)(Kh + row0 * p.k_ss), 0, kbytes,
+                                                      kBufferWord3);
+    const auto vr = __builtin_amdgcn_make_buffer_rsrc((void*)(Vh + row0 * p.v_ss), 0, vbytes,
+                                                      kBufferWord3);
 #pragma unroll
     for (int i = 0; i < PER_T; ++i) {
       kd[i] = __builtin_bit_cast(uint4_t, __builtin_amdgcn_raw_buffer_load_b128(kr, kvo[i], 0, 0));
@@ -285,57 +297,61 @@ void prefill_kernel(PrefillParams p) {
     voff[n] = TILEB + vrow * ROWB + (((4 * n + vcl) ^ swz(vrow)) * 16) + (s16 & 1) * 8;
 
   // ---- Q^T fragments of the two 32-row blocks: lane -> row, dims g*HALF + 8s + e.
-  half8_t qf[2][KS];
+  half8_t qf[NRB][KS];
 #pragma unroll
-  for (int rb = 0; rb < 2; ++rb) {
+  for (int rb = 0; rb < NRB; ++rb) {
     const int row = r0 + 32 * rb + l32;
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
       uint4_t v = {0, 0, 0, 0};
       // Var-len query rows at or past the length are read as zeros: their
-      // outputs are unspecified, and non-finite padding must not reach the
-      // row sums, whose MFMA pairs row n with row n + 16.
+      // outputs are unspecified, and non-finite padding is kept out of every
+      // computation.
       if (active && row < (VARLEN ? len : S)) v = ld16(Qh + (int64_t)row * p.q_ss + g * HALF + 8 * s);
       qf[rb][s] = as_half8(v);
     }
   }
 
-  float16_t oacc[2][NT];
+  float16_t oacc[NRB][NT];
 #pragma unroll
-  for (int rb = 0; rb < 2; ++rb)
+  for (int rb = 0; rb < NRB; ++rb)
 #pragma unroll
     for (int n = 0; n < NT; ++n)
 #pragma unroll
       for (int r = 0; r < 16; ++r) oacc[rb][n][r] = 0.f;
-  float m_run[2] = {AKT_P_NEG_INF, AKT_P_NEG_INF};
-  float l_part[2] = {0.f, 0.f};
+  float m_run[NRB], l_part[NRB];
+#pragma unroll
+  for (int rb = 0; rb < NRB; ++rb) {
+    m_run[rb] = AKT_P_NEG_INF;
+    l_part[rb] = 0.f;
+  }
   const float c = p.qk_scale;
   const uint32_t kOnes = 0x3c003c00u;
   // Per-lane causal / length limit: element r of a step's S^T holds key
   // kh0 + 8 (r / 4) + 4 g + r % 4 of row r0 + 32 rb + l32.
-  int lim_base[2];
+  int lim_base[NRB];
 #pragma unroll
-  for (int rb = 0; rb < 2; ++rb) {
+  for (int rb = 0; rb < NRB; ++rb) {
     const int row = r0 + 32 * rb + l32;
     lim_base[rb] = (CAUSAL ? min(row, S - 1) : S - 1) - 4 * g;
   }
 
-  float16_t sA[2], sB[2];
-  uint32_t pA[2][8], pB[2][8];  // pB starts as P(-1) = 0; pA is written before it is read
+  float16_t sA[NRB], sB[NRB];
+  uint32_t pA[NRB][8], pB[NRB][8];  // pB starts as P(-1) = 0; pA is written before it is read
   half8_t vf[2][NT];            // V fragments for the next P.V
 #pragma unroll
-  for (int rb = 0; rb < 2; ++rb)
+  for (int rb = 0; rb < NRB; ++rb)
 #pragma unroll
     for (int i = 0; i < 8; ++i) pB[rb][i] = 0u;
 
   // Fragment reads of 32-key step t (its tile must be published).
   auto load_kf = [&](int t, half8_t (&kf)[KS]) {
-    const char* kb = lds + ((t >> 1) % kNBuf) * BUFB + (t & 1) * 32 * ROWB;
+    const char* kb = lds + ((t / SPT) % kNBuf) * BUFB + (t % SPT) * 32 * ROWB;
 #pragma unroll
     for (int s = 0; s < KS; ++s) kf[s] = as_half8(*reinterpret_cast<const uint4_t*>(kb + koff[s]));
   };
   auto load_vf = [&](int t, half8_t (&vf)[2][NT]) {
-    const char* vb = lds + ((t >> 1) % kNBuf) * BUFB + (t & 1) * 32 * ROWB;
+    const char* vb = lds + ((t / SPT) % kNBuf) * BUFB + (t % SPT) * 32 * ROWB;
 #pragma unroll
     for (int u = 0; u < 2; ++u)
 #pragma unroll
@@ -347,56 +363,49 @@ void prefill_kernel(PrefillParams p) {
       }
   };
   // S^T = K . Q^T for one step.
-  auto qk_mfma = [&](const half8_t (&kf)[KS], float16_t (&sdst)[2]) {
+  auto qk_mfma = [&](const half8_t (&kf)[KS], float16_t (&sdst)[NRB]) {
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb)
+    for (int rb = 0; rb < NRB; ++rb)
 #pragma unroll
       for (int r = 0; r < 16; ++r) sdst[rb][r] = 0.f;
 #pragma unroll
     for (int s = 0; s < KS; ++s)
 #pragma unroll
-      for (int rb = 0; rb < 2; ++rb) sdst[rb] = mfma32x32x16(kf[s], qf[rb][s], sdst[rb]);
+      for (int rb = 0; rb < NRB; ++rb) sdst[rb] = mfma32x32x16(kf[s], qf[rb][s], sdst[rb]);
   };
   // O^T += V^T . P^T for one step.
-  auto pv_mfma = [&](const half8_t (&vf)[2][NT], const uint32_t (&pk)[2][8]) {
+  auto pv_mfma = [&](const half8_t (&vf)[2][NT], const uint32_t (&pk)[NRB][8]) {
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
-      half8_t bop[2];
+      half8_t bop[NRB];
 #pragma unroll
-      for (int rb = 0; rb < 2; ++rb)
+      for (int rb = 0; rb < NRB; ++rb)
         bop[rb] = as_half8(uint4_t{pk[rb][4 * u], pk[rb][4 * u + 1], pk[rb][4 * u + 2],
                                    pk[rb][4 * u + 3]});
 #pragma unroll
       for (int n = 0; n < NT; ++n)
 #pragma unroll
-        for (int rb = 0; rb < 2; ++rb) oacc[rb][n] = mfma32x32x16(vf[u][n], bop[rb], oacc[rb][n]);
+        for (int rb = 0; rb < NRB; ++rb) oacc[rb][n] = mfma32x32x16(vf[u][n], bop[rb], oacc[rb][n]);
     }
   };
-  auto qk = [&](int t, float16_t (&sdst)[2]) {
+  auto qk = [&](int t, float16_t (&sdst)[NRB]) {
     half8_t kf[KS];
     load_kf(t, kf);
     qk_mfma(kf, sdst);
   };
-  auto pv = [&](int t, const uint32_t (&pk)[2][8]) {
+  auto pv = [&](int t, const uint32_t (&pk)[NRB][8]) {
     half8_t vf[2][NT];
     load_vf(t, vf);
     pv_mfma(vf, pk);
   };
   // Probabilities of S(t) against the running max m_run: fp16-rounded P into
-  // pk and the step's row sums into l_step.
-  // The row sums of P run on the matrix pipe: a v_mfma_f32_16x16x32_f16 takes
-  // a 16-key P^T fragment as its B operand unchanged (lane L then stands for
-  // row L & 15 + 16 ((L >> 4) & 1) and keys 8 (L >> 5) ..), and the 0/1 A
-  // operand ones_a picks, for output rows m < 8, the lanes of rows 0..15 and,
-  // for m >= 8, those of rows 16..31.  Summed over the step's two fragments,
-  // lane L's result is the full 32-key sum of row
-  // rho = (L & 15) + 16 (L >> 5); l_part keeps that layout.
-  const uint32_t ones_bits = ((((lane >> 4) & 1) == 0) == ((lane & 15) < 8)) ? kOnes : 0u;
-  const half8_t ones_a = as_half8(uint4_t{ones_bits, ones_bits, ones_bits, ones_bits});
-  const int rho = (lane & 15) + 16 * (lane >> 5);
-  auto softmax = [&](const float16_t (&ss)[2], uint32_t (&pk)[2][8], float (&l_step)[2]) {
+  // pk and, in l_step, each lane's sum of the 16 rounded probabilities it
+  // holds: row l32's keys of lane half g (v_dot2 against ones on the VALU, so
+  // every row's sum is its own).  l_part keeps these half-row sums; the two
+  // halves are added once, for the output.
+  auto softmax = [&](const float16_t (&ss)[NRB], uint32_t (&pk)[NRB][8], float (&l_step)[NRB]) {
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb) {
+    for (int rb = 0; rb < NRB; ++rb) {
 #pragma unroll
       for (int r = 0; r < 16; r += 2) {
         const float p0 = fast_exp2(__builtin_fmaf(ss[rb][r], c, -m_run[rb]));
@@ -405,21 +414,21 @@ void prefill_kernel(PrefillParams p) {
       }
     }
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb) {
-      float4_t ls = {0.f, 0.f, 0.f, 0.f};
-      ls = mfma16x16x32(ones_a, as_half8(uint4_t{pk[rb][0], pk[rb][1], pk[rb][2], pk[rb][3]}), ls);
-      ls = mfma16x16x32(ones_a, as_half8(uint4_t{pk[rb][4], pk[rb][5], pk[rb][6], pk[rb][7]}), ls);
-      l_step[rb] = ls[0];
+    for (int rb = 0; rb < NRB; ++rb) {
+      float ls = 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) ls = dot2(pk[rb][i], kOnes, ls);
+      l_step[rb] = ls;
     }
   };
   // Masks S(t): keys past a row (causal) or past S read -inf.  The test is
   // wave-uniform; only the steps that reach the diagonal or S run the
   // selects.
-  auto mask_step = [&](int t, float16_t (&ss)[2]) {
+  auto mask_step = [&](int t, float16_t (&ss)[NRB]) {
     const int kh0 = t * 32;
     if ((CAUSAL && kh0 + 31 > r0) || kh0 + 32 > S) {
 #pragma unroll
-      for (int rb = 0; rb < 2; ++rb) {
+      for (int rb = 0; rb < NRB; ++rb) {
         const int lim = lim_base[rb] - kh0;
 #pragma unroll
         for (int r = 0; r < 16; ++r)
@@ -450,8 +459,8 @@ void prefill_kernel(PrefillParams p) {
   // computed on the old max, has been accumulated) and the step's
   // probabilities are recomputed.  Otherwise every P stays below
   // 32 * 2^kRescaleSlack, far inside fp16's range.
-  auto step = [&](int t, float16_t (&scur)[2], float16_t (&snext)[2],
-                  const uint32_t (&pprev)[2][8], uint32_t (&pcur)[2][8]) {
+  auto step = [&](int t, float16_t (&scur)[NRB], float16_t (&snext)[NRB],
+                  const uint32_t (&pprev)[NRB][8], uint32_t (&pcur)[NRB][8]) {
     mask_step(t, scur);  // S(0) was masked before the loop too: masking is idempotent
     half8_t kf[KS];
     if constexpr (!kPrefetchV) load_vf(t > 0 ? t - 1 : 0, vf);
@@ -462,26 +471,26 @@ void prefill_kernel(PrefillParams p) {
     // V of step t, for P.V(t) at the top of step t + 1 (its tile is published).
     if constexpr (kPrefetchV) load_vf(t, vf);
 
-    float l_step[2];
+    float l_step[NRB];
     softmax(scur, pcur, l_step);
     // Issue order of the region: each of the 16 P.V / QK MFMAs followed by
     // three VALU instructions, so one wave alternates its matrix and vector
     // work instead of issuing them in clusters (2% per tile, measured).
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
+    for (int i = 0; i < (D >= 192 ? 2 * D / 16 : 16); ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
       __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // three VALU
     }
     bool over = false;
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb) over |= !(l_step[rb] <= kStepSumLimit);
+    for (int rb = 0; rb < NRB; ++rb) over |= !(l_step[rb] <= kStepSumLimit);
     if (__any(over)) {  // wave-uniform, rare
 #pragma unroll
-      for (int rb = 0; rb < 2; ++rb) {
+      for (int rb = 0; rb < NRB; ++rb) {
         const float mx = row_max(scur[rb]);
         const bool raise = mx > m_run[rb] + kRescaleSlack;
         const float alpha = raise ? fast_exp2(m_run[rb] - mx) : 1.f;
-        l_part[rb] *= __shfl(alpha, rho, 64);  // row rho's factor (lane rho < 32 holds it)
+        l_part[rb] *= alpha;  // this lane's row
         if (raise) {
           m_run[rb] = mx;
 #pragma unroll
@@ -493,7 +502,7 @@ void prefill_kernel(PrefillParams p) {
       softmax(scur, pcur, l_step);
     }
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb) l_part[rb] += l_step[rb];
+    for (int rb = 0; rb < NRB; ++rb) l_part[rb] += l_step[rb];
   };
 
   // Tiles 0..2 and Q are requested together (one round trip); tiles 0 and 1
@@ -515,22 +524,27 @@ void prefill_kernel(PrefillParams p) {
   if constexpr (kPrefetchV) load_vf(0, vf);  // P.V(-1) of step 0 multiplies P = 0
   mask_step(0, sA);
 #pragma unroll
-  for (int rb = 0; rb < 2; ++rb) m_run[rb] = row_max(sA[rb]);
-  // Steps run in pairs (2j, 2j + 1), one pair per tile; n_h is even.  At the
-  // top of pair j: sA = S(2j) and pB = P(2j - 1) (zero for j = 0).  The last
-  // pair's S(2j + 2) is computed from whatever its buffer holds and never
-  // used; the pair is followed by the drain P.V(2j + 1).
-#pragma clang loop unroll(disable)
-  for (int j = 0; j < n_tiles; ++j) {
-    // Publishes tile j + 1 (stored before the previous barrier) and retires
-    // the buffer of tile j - 2, which now takes tile j + 2 from the staging
-    // registers; tile j + 3 is then fetched into them.
+  for (int rb = 0; rb < NRB; ++rb) m_run[rb] = row_max(sA[rb]);
+  // Publishes tile j + 1 (stored before the previous barrier) and retires the
+  // buffer of tile j - 2, which now takes tile j + 2 from the staging
+  // registers; tile j + 3 is then fetched into them.  Step t reads K of step
+  // t + 1 and V of step t - 1, so a step's turn comes at its own tile.
+  auto tile_turn = [&](int j) {
     __syncthreads();
     if (j + 2 < n_tiles) store_tile(j + 2);
     if (j + 3 < n_tiles) load_tile(j + 3);
-    const int t = 2 * j;
-    if (t < n_h) {  // wave-uniform
-      step(t, sA, sB, pB, pA);
+  };
+  // Steps run in pairs (t, t + 1) (one tile of two steps, or two tiles of one
+  // step); n_h is even.  At the top of a pair: sA = S(t) and pB = P(t - 1)
+  // (zero for t = 0).  The last pair's S(t + 2) is computed from whatever its
+  // buffer holds and never used; the pair is followed by the drain P.V(t + 1).
+#pragma clang loop unroll(disable)
+  for (int j = 0; j < n_tiles; j += 2 / SPT) {
+    tile_turn(j);
+    const int t = SPT * j;
+    if (t < n_h) step(t, sA, sB, pB, pA);  // wave-uniform
+    if constexpr (SPT == 1) tile_turn(j + 1);  // n_tiles is even
+    if (t < n_h) {
       step(t + 1, sB, sA, pA, pB);
       if (t + 2 == n_h) {  // drain: P.V(n_h - 1)
         if constexpr (kPrefetchV) pv_mfma(vf, pB);
@@ -545,11 +559,11 @@ void prefill_kernel(PrefillParams p) {
   int lane_e = lane;
   asm volatile("" : "+v"(lane_e));
 #pragma unroll
-  for (int rb = 0; rb < 2; ++rb) {
+  for (int rb = 0; rb < NRB; ++rb) {
     const int row = r0 + 32 * rb + (lane_e & 31);
     if (row >= row_lim) continue;
     // Row l32's normaliser sits in lane l32 (rows 0..15) or l32 + 16.
-    const float l_row = __shfl(l_part[rb], l32 < 16 ? l32 : l32 + 16, 64);
+    const float l_row = xor32_sum(l_part[rb]);  // both key halves of row l32
     const float inv = l_row > 0.f ? __builtin_amdgcn_rcpf(l_row) : 0.f;
     if (p.lse && g == 0) {
       // ln sum_k exp(scale * q.k) = (m + log2 l) * ln 2: P = exp2(c s - m) and
@@ -600,8 +614,9 @@ int prefill_impl(const void* q, const void* k, const void* v, void* o, float* ls
   AKT_CHECK(num_q_heads % num_kv_heads == 0,
             "num_q_heads (%lld) must be a multiple of num_kv_heads (%lld)", (long long)num_q_heads,
             (long long)num_kv_heads);
-  if (head_dim != 64 && head_dim != 128)
-    return set_error(AKT_ERR_UNSUPPORTED, "prefill head_dim %lld not supported (64, 128)",
+  if (head_dim != 64 && head_dim != 128 && head_dim != 192 && head_dim != 256)
+    return set_error(AKT_ERR_UNSUPPORTED,
+                     "prefill head_dim %lld not supported (64, 128, 192, 256)",
                      (long long)head_dim);
   AKT_CHECK(seq_len >= 0 && seq_len < (1ll << 30), "seq_len out of range");
   AKT_CHECK(q_stride[3] == 1 && k_stride[3] == 1 && v_stride[3] == 1 && o_stride[3] == 1,
@@ -640,7 +655,7 @@ int prefill_impl(const void* q, const void* k, const void* v, void* o, float* ls
   p.Hkv = (int)num_kv_heads;
   p.G = (int)(num_q_heads / num_kv_heads);
   p.S = (int)seq_len;
-  p.n_rb = (int)ceil_div(seq_len, kRows);
+  p.n_rb = (int)ceil_div(seq_len, rows_for((int)head_dim));
   p.n_sg = (int)ceil_div((int64_t)p.G * p.n_rb, kSlots);
   p.grid1d = (batch > 65535 || p.n_sg > 65535) ? 1 : 0;
   p.fast_div = ((int64_t)p.G * p.n_rb + kSlots < (1ll << 22)) ? 1 : 0;
@@ -654,7 +669,9 @@ int prefill_impl(const void* q, const void* k, const void* v, void* o, float* ls
   const bool is_var = varlen != nullptr;
   hipStream_t st = (hipStream_t)stream;
   if (head_dim == 64) return launch_d<64>(is_causal, is_var, p, grid, st);
-  return launch_d<128>(is_causal, is_var, p, grid, st);
+  if (head_dim == 128) return launch_d<128>(is_causal, is_var, p, grid, st);
+  if (head_dim == 192) return launch_d<192>(is_causal, is_var, p, grid, st);
+  return launch_d<256>(is_causal, is_var, p, grid, st);
 }
 }  // namespace
 
