@@ -8,6 +8,8 @@
 #include <stdint.h>
 #include <stdio.h>
 
+#include <atomic>
+
 #include "../../include/akt_amd.h"
 
 namespace akt {
@@ -62,6 +64,28 @@ inline bool rows_aligned16(const void* base, const int64_t* strides, int n) {
 
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 inline int64_t round_up(int64_t a, int64_t b) { return ceil_div(a, b) * b; }
+
+constexpr int kMaxResidentDevices = 64;
+
+// Workgroups of `kernel` (blocks of `threads`) that fit the current device at
+// once (occupancy x CUs), cached per kernel instance and device; 0 if the
+// queries fail.
+template <typename Kernel>
+int resident_blocks(Kernel kernel, int threads) {
+  static std::atomic<int> cache[kMaxResidentDevices];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxResidentDevices) return 0;
+  int v = cache[dev].load(std::memory_order_relaxed);
+  if (v > 0) return v;
+  int per_cu = 0, cus = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void*)kernel, threads, 0) !=
+          hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    return 0;
+  v = (per_cu > 0 ? per_cu : 1) * (cus > 0 ? cus : 1);
+  cache[dev].store(v, std::memory_order_relaxed);
+  return v;
+}
 
 }  // namespace akt
 

@@ -1032,25 +1032,6 @@ int pick_gt(int G, int D) {
   return gt;
 }
 
-// Workgroups of `kernel` that fit the current device at once (occupancy x CUs),
-// cached per kernel instance and device.
-template <typename Kernel>
-int resident_blocks(Kernel kernel) {
-  static std::atomic<int> cache[kMaxDevices];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 0;
-  int v = cache[dev].load(std::memory_order_relaxed);
-  if (v > 0) return v;
-  int per_cu = 0, cus = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void*)kernel, kThreads, 0) !=
-          hipSuccess ||
-      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-    return 0;
-  v = (per_cu > 0 ? per_cu : 1) * (cus > 0 ? cus : 1);
-  cache[dev].store(v, std::memory_order_relaxed);
-  return v;
-}
-
 // Launches one split-kernel instance.  Persistent instances get a grid of
 // min(items, resident workgroups); `grid` carries the item upper bound in x.
 template <int D, int GT, int MODE, bool ALIGNED, bool MAGIC, int GPW, bool PERSIST>
@@ -1058,7 +1039,7 @@ int launch_split(const SplitParams& p, dim3 grid, hipStream_t st) {
   auto kernel = split_kernel<D, GT, MODE, ALIGNED, MAGIC, GPW, PERSIST>;
   if (PERSIST) {
     const int64_t items = (int64_t)grid.x * grid.y;
-    const int cap = resident_blocks(kernel);
+    const int cap = resident_blocks(kernel, kThreads);
     if (cap <= 0) return set_error(AKT_ERR_HIP, "occupancy query failed");
     grid = dim3((unsigned)(items < cap ? items : cap), 1);
   }

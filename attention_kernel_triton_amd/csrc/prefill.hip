@@ -473,13 +473,15 @@ void prefill_kernel(PrefillParams p) {
 
     float l_step[NRB];
     softmax(scur, pcur, l_step);
-    // Issue order of the region: each of the 16 P.V / QK MFMAs followed by
-    // three VALU instructions, so one wave alternates its matrix and vector
-    // work instead of issuing them in clusters (2% per tile, measured).
+    // Issue order of the region: each P.V / QK MFMA followed by two VALU
+    // instructions, so one wave alternates its matrix and vector work instead
+    // of issuing them in clusters.  Two per MFMA, not more: the wave issues in
+    // order, and a longer VALU run between MFMAs (three) left the matrix pipe
+    // idle at D = 128 (16% slower there, the same at D = 64 and 256).
 #pragma unroll
     for (int i = 0; i < (D >= 192 ? 2 * D / 16 : 16); ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
-      __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // three VALU
+      __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // two VALU
     }
     bool over = false;
 #pragma unroll
@@ -553,26 +555,36 @@ void prefill_kernel(PrefillParams p) {
     }
   }
 
+  // ---- epilogue: O is normalised, transposed through LDS and written as
+  // whole rows.  Each lane holds 4-element pieces of one row, so writing them
+  // straight to HBM costs one store instruction per piece, each spread over
+  // 32 rows; through LDS every lane stores 16 contiguous bytes and a wave
+  // stores whole rows.  The barrier retires every tile buffer first (all
+  // waves pass it: the loop's turn count is the workgroup's).
+  __syncthreads();
   if (!active) return;
   // The row index is derived again here (the opaque copy keeps the compiler
   // from holding the prologue's row registers live through the loop).
   int lane_e = lane;
   asm volatile("" : "+v"(lane_e));
+  static_assert(kSlots * kRows * ROWB <= kNBuf * BUFB, "O staging fits the tile buffers");
+  char* ost = lds + wave * (kRows * ROWB);  // this wave's rows, 16-byte chunks swizzled
 #pragma unroll
   for (int rb = 0; rb < NRB; ++rb) {
-    const int row = r0 + 32 * rb + (lane_e & 31);
-    if (row >= row_lim) continue;
+    const int lr = 32 * rb + (lane_e & 31);  // row within the wave's block
+    const int row = r0 + lr;
     // Row l32's normaliser sits in lane l32 (rows 0..15) or l32 + 16.
     const float l_row = xor32_sum(l_part[rb]);  // both key halves of row l32
     const float inv = l_row > 0.f ? __builtin_amdgcn_rcpf(l_row) : 0.f;
-    if (p.lse && g == 0) {
+    if (p.lse && g == 0 && row < row_lim) {
       // ln sum_k exp(scale * q.k) = (m + log2 l) * ln 2: P = exp2(c s - m) and
       // l sums the fp16-rounded P (the reference's commented-out store at
       // prefill_flash_attention.py:331-333 is m + log l in natural units).
       p.lse[(int64_t)b * p.lse_sb + (int64_t)h * p.lse_sh + (int64_t)row * p.lse_ss] =
           l_row > 0.f ? (m_run[rb] + __log2f(l_row)) * kLn2 : AKT_P_NEG_INF;
     }
-    half_t* orow = Oh + (int64_t)row * p.o_ss;
+    // Element r of oacc[rb][n] is dim 32 n + 8 (r / 4) + 4 g + r % 4: half of
+    // 16-byte chunk 4 n + r / 4.
 #pragma unroll
     for (int n = 0; n < NT; ++n)
 #pragma unroll
@@ -580,8 +592,18 @@ void prefill_kernel(PrefillParams p) {
         half4_t hv;
 #pragma unroll
         for (int r = 0; r < 4; ++r) hv[r] = (half_t)(oacc[rb][n][4 * q4 + r] * inv);
-        *reinterpret_cast<half4_t*>(orow + 32 * n + 8 * q4 + 4 * g) = hv;
+        const int chunk = (4 * n + q4) ^ swz(lr);
+        *reinterpret_cast<half4_t*>(ost + lr * ROWB + chunk * 16 + 8 * g) = hv;
       }
+  }
+  // Row-major read back: lane i takes chunk i % CPR of row i / CPR (+ 64 / CPR
+  // rows per pass); the LDS writes above are this wave's own and complete in order.
+#pragma unroll
+  for (int idx = lane_e; idx < kRows * CPR; idx += 64) {
+    const int lr = idx / CPR, cc = idx % CPR;
+    const uint4_t v = *reinterpret_cast<const uint4_t*>(ost + lr * ROWB + ((cc ^ swz(lr)) * 16));
+    const int row = r0 + lr;
+    if (row < row_lim) *reinterpret_cast<uint4_t*>(Oh + (int64_t)row * p.o_ss + 8 * cc) = v;
   }
 }
 
