@@ -30,6 +30,9 @@ _SIGNATURES = {
     "akt_prefill_fwd_lse": (C.c_int, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64,
                                       _i64x, _i64x, _i64x, _i64x, _i64x, C.c_float, C.c_int, _p,
                                       C.c_int, _p]),
+    "akt_prefill_fwd_ex": (C.c_int, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64,
+                                     _i64x, _i64x, _i64x, _i64x, _i64x, C.c_float, C.c_int, _p,
+                                     C.c_int, C.c_int, _p]),
     "akt_merge_states": (C.c_int, [_p, C.c_int, _p, _p, C.c_int, _p, _i64, _i64, _i64, _i64x,
                                    _i64x, _i64, _i64, _p]),
     "akt_decode_workspace_size": (C.c_size_t, [_i64, _i64, _i64, _i64, _i64, _i64]),

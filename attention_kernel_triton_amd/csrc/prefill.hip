@@ -3,8 +3,8 @@
 // Replaces the reference's Triton prefill kernels
 //   prefill_flash_attention.py:18-335                   (dense)
 //   prefill_flash_attention_var_len_padding.py:109-341  (right-padded var-len)
-// with an MFMA kernel designed around CDNA4's v_mfma_f32_32x32x16_f16 and its
-// transposing LDS read (ds_read_b64_tr_b16).
+// with an MFMA kernel designed around CDNA4's v_mfma_f32_32x32x16_f16 (or its
+// bf16 form for bf16 tensors) and the transposing LDS read (ds_read_b64_tr_b16).
 //
 // Work decomposition.  A 256-thread workgroup serves one (batch, kv head) and
 // four "slots"; slot f = (query head f % G, 64-row block f / G) of that kv
@@ -115,6 +115,37 @@ __device__ __forceinline__ uint2 ds_read_tr16(const char* lds_ptr) {
   return __builtin_bit_cast(uint2, r);
 }
 
+// Operand element type of a kernel instance: fp16 (v_mfma_f32_32x32x16_f16,
+// P rounded to fp16 as the reference does) or bf16 (the bf16 MFMA, P rounded
+// to bf16, since both MFMA operands share one type).  Global loads and the
+// LDS staging move raw 16-byte chunks and do not depend on it.
+template <bool BF16>
+struct Elt {
+  typedef half8_t v8;
+  static constexpr uint32_t kOnes = 0x3c003c00u;  // (1, 1)
+  static __device__ __forceinline__ v8 as8(uint4_t u) { return __builtin_bit_cast(v8, u); }
+  static __device__ __forceinline__ float16_t mfma(v8 a, v8 b, float16_t c) {
+    return mfma32x32x16(a, b, c);
+  }
+  static __device__ __forceinline__ uint32_t pack2(float lo, float hi) { return pack_half2(lo, hi); }
+  static __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+    return ::akt::dot2(a, b, c);
+  }
+};
+template <>
+struct Elt<true> {
+  typedef bf16x8_t v8;
+  static constexpr uint32_t kOnes = 0x3f803f80u;  // (1, 1)
+  static __device__ __forceinline__ v8 as8(uint4_t u) { return __builtin_bit_cast(v8, u); }
+  static __device__ __forceinline__ float16_t mfma(v8 a, v8 b, float16_t c) {
+    return mfma32x32x16_bf16(a, b, c);
+  }
+  static __device__ __forceinline__ uint32_t pack2(float lo, float hi) { return pack_bf16x2(lo, hi); }
+  static __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+    return dot2_bf16(a, b, c);
+  }
+};
+
 // Chunk-position swizzle of a tile row (see the header comment).  Any 8
 // consecutive rows get distinct values, and rows 4i..4i+3 get values that
 // differ in bits 1..2.
@@ -156,9 +187,11 @@ __device__ __forceinline__ int div_small(int n, int d, float inv) {
   return q;
 }
 
-template <int D, bool CAUSAL, bool VARLEN>
+template <int D, bool CAUSAL, bool VARLEN, bool BF16>
 __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(D == 64 ? 2 : 1, 2)))
 void prefill_kernel(PrefillParams p) {
+  typedef Elt<BF16> E;
+  typedef typename E::v8 v8;
   constexpr int NRB = rblocks_for(D);     // 32-row MFMA blocks per wave
   constexpr int kRows = rows_for(D);      // query rows per slot
   constexpr int kBN = tile_keys_for(D);   // keys per staged tile
@@ -297,7 +330,7 @@ void prefill_kernel(PrefillParams p) {
     voff[n] = TILEB + vrow * ROWB + (((4 * n + vcl) ^ swz(vrow)) * 16) + (s16 & 1) * 8;
 
   // ---- Q^T fragments of the two 32-row blocks: lane -> row, dims g*HALF + 8s + e.
-  half8_t qf[NRB][KS];
+  v8 qf[NRB][KS];
 #pragma unroll
   for (int rb = 0; rb < NRB; ++rb) {
     const int row = r0 + 32 * rb + l32;
@@ -308,7 +341,7 @@ void prefill_kernel(PrefillParams p) {
       // outputs are unspecified, and non-finite padding is kept out of every
       // computation.
       if (active && row < (VARLEN ? len : S)) v = ld16(Qh + (int64_t)row * p.q_ss + g * HALF + 8 * s);
-      qf[rb][s] = as_half8(v);
+      qf[rb][s] = E::as8(v);
     }
   }
 
@@ -326,7 +359,6 @@ void prefill_kernel(PrefillParams p) {
     l_part[rb] = 0.f;
   }
   const float c = p.qk_scale;
-  const uint32_t kOnes = 0x3c003c00u;
   // Per-lane causal / length limit: element r of a step's S^T holds key
   // kh0 + 8 (r / 4) + 4 g + r % 4 of row r0 + 32 rb + l32.
   int lim_base[NRB];
@@ -338,19 +370,19 @@ void prefill_kernel(PrefillParams p) {
 
   float16_t sA[NRB], sB[NRB];
   uint32_t pA[NRB][8], pB[NRB][8];  // pB starts as P(-1) = 0; pA is written before it is read
-  half8_t vf[2][NT];            // V fragments for the next P.V
+  v8 vf[2][NT];                 // V fragments for the next P.V
 #pragma unroll
   for (int rb = 0; rb < NRB; ++rb)
 #pragma unroll
     for (int i = 0; i < 8; ++i) pB[rb][i] = 0u;
 
   // Fragment reads of 32-key step t (its tile must be published).
-  auto load_kf = [&](int t, half8_t (&kf)[KS]) {
+  auto load_kf = [&](int t, v8 (&kf)[KS]) {
     const char* kb = lds + ((t / SPT) % kNBuf) * BUFB + (t % SPT) * 32 * ROWB;
 #pragma unroll
-    for (int s = 0; s < KS; ++s) kf[s] = as_half8(*reinterpret_cast<const uint4_t*>(kb + koff[s]));
+    for (int s = 0; s < KS; ++s) kf[s] = E::as8(*reinterpret_cast<const uint4_t*>(kb + koff[s]));
   };
-  auto load_vf = [&](int t, half8_t (&vf)[2][NT]) {
+  auto load_vf = [&](int t, v8 (&vf)[2][NT]) {
     const char* vb = lds + ((t / SPT) % kNBuf) * BUFB + (t % SPT) * 32 * ROWB;
 #pragma unroll
     for (int u = 0; u < 2; ++u)
@@ -359,11 +391,11 @@ void prefill_kernel(PrefillParams p) {
         const char* vp = vb + voff[n] + u * 16 * ROWB;
         const uint2 lo = ds_read_tr16(vp);
         const uint2 hi = ds_read_tr16(vp + 8 * ROWB);
-        vf[u][n] = as_half8(uint4_t{lo.x, lo.y, hi.x, hi.y});
+        vf[u][n] = E::as8(uint4_t{lo.x, lo.y, hi.x, hi.y});
       }
   };
   // S^T = K . Q^T for one step.
-  auto qk_mfma = [&](const half8_t (&kf)[KS], float16_t (&sdst)[NRB]) {
+  auto qk_mfma = [&](const v8 (&kf)[KS], float16_t (&sdst)[NRB]) {
 #pragma unroll
     for (int rb = 0; rb < NRB; ++rb)
 #pragma unroll
@@ -371,36 +403,36 @@ void prefill_kernel(PrefillParams p) {
 #pragma unroll
     for (int s = 0; s < KS; ++s)
 #pragma unroll
-      for (int rb = 0; rb < NRB; ++rb) sdst[rb] = mfma32x32x16(kf[s], qf[rb][s], sdst[rb]);
+      for (int rb = 0; rb < NRB; ++rb) sdst[rb] = E::mfma(kf[s], qf[rb][s], sdst[rb]);
   };
   // O^T += V^T . P^T for one step.
-  auto pv_mfma = [&](const half8_t (&vf)[2][NT], const uint32_t (&pk)[NRB][8]) {
+  auto pv_mfma = [&](const v8 (&vf)[2][NT], const uint32_t (&pk)[NRB][8]) {
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
-      half8_t bop[NRB];
+      v8 bop[NRB];
 #pragma unroll
       for (int rb = 0; rb < NRB; ++rb)
-        bop[rb] = as_half8(uint4_t{pk[rb][4 * u], pk[rb][4 * u + 1], pk[rb][4 * u + 2],
-                                   pk[rb][4 * u + 3]});
+        bop[rb] = E::as8(uint4_t{pk[rb][4 * u], pk[rb][4 * u + 1], pk[rb][4 * u + 2],
+                                 pk[rb][4 * u + 3]});
 #pragma unroll
       for (int n = 0; n < NT; ++n)
 #pragma unroll
-        for (int rb = 0; rb < NRB; ++rb) oacc[rb][n] = mfma32x32x16(vf[u][n], bop[rb], oacc[rb][n]);
+        for (int rb = 0; rb < NRB; ++rb) oacc[rb][n] = E::mfma(vf[u][n], bop[rb], oacc[rb][n]);
     }
   };
   auto qk = [&](int t, float16_t (&sdst)[NRB]) {
-    half8_t kf[KS];
+    v8 kf[KS];
     load_kf(t, kf);
     qk_mfma(kf, sdst);
   };
   auto pv = [&](int t, const uint32_t (&pk)[NRB][8]) {
-    half8_t vf[2][NT];
+    v8 vf[2][NT];
     load_vf(t, vf);
     pv_mfma(vf, pk);
   };
-  // Probabilities of S(t) against the running max m_run: fp16-rounded P into
-  // pk and, in l_step, each lane's sum of the 16 rounded probabilities it
-  // holds: row l32's keys of lane half g (v_dot2 against ones on the VALU, so
+  // Probabilities of S(t) against the running max m_run: P rounded to the
+  // operand type into pk and, in l_step, each lane's sum of the 16 rounded
+  // probabilities it holds: row l32's keys of lane half g (v_dot2 against ones on the VALU, so
   // every row's sum is its own).  l_part keeps these half-row sums; the two
   // halves are added once, for the output.
   auto softmax = [&](const float16_t (&ss)[NRB], uint32_t (&pk)[NRB][8], float (&l_step)[NRB]) {
@@ -410,14 +442,14 @@ void prefill_kernel(PrefillParams p) {
       for (int r = 0; r < 16; r += 2) {
         const float p0 = fast_exp2(__builtin_fmaf(ss[rb][r], c, -m_run[rb]));
         const float p1 = fast_exp2(__builtin_fmaf(ss[rb][r + 1], c, -m_run[rb]));
-        pk[rb][r >> 1] = pack_half2(p0, p1);
+        pk[rb][r >> 1] = E::pack2(p0, p1);
       }
     }
 #pragma unroll
     for (int rb = 0; rb < NRB; ++rb) {
       float ls = 0.f;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) ls = dot2(pk[rb][i], kOnes, ls);
+      for (int i = 0; i < 8; ++i) ls = E::dot2(pk[rb][i], E::kOnes, ls);
       l_step[rb] = ls;
     }
   };
@@ -462,7 +494,7 @@ void prefill_kernel(PrefillParams p) {
   auto step = [&](int t, float16_t (&scur)[NRB], float16_t (&snext)[NRB],
                   const uint32_t (&pprev)[NRB][8], uint32_t (&pcur)[NRB][8]) {
     mask_step(t, scur);  // S(0) was masked before the loop too: masking is idempotent
-    half8_t kf[KS];
+    v8 kf[KS];
     if constexpr (!kPrefetchV) load_vf(t > 0 ? t - 1 : 0, vf);
     load_kf(t + 1, kf);
 
@@ -589,11 +621,11 @@ void prefill_kernel(PrefillParams p) {
     for (int n = 0; n < NT; ++n)
 #pragma unroll
       for (int q4 = 0; q4 < 4; ++q4) {
-        half4_t hv;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) hv[r] = (half_t)(oacc[rb][n][4 * q4 + r] * inv);
+        const float16_t& a = oacc[rb][n];
+        const uint2 hv = {E::pack2(a[4 * q4] * inv, a[4 * q4 + 1] * inv),
+                          E::pack2(a[4 * q4 + 2] * inv, a[4 * q4 + 3] * inv)};
         const int chunk = (4 * n + q4) ^ swz(lr);
-        *reinterpret_cast<half4_t*>(ost + lr * ROWB + chunk * 16 + 8 * g) = hv;
+        *reinterpret_cast<uint2*>(ost + lr * ROWB + chunk * 16 + 8 * g) = hv;
       }
   }
   // Row-major read back: lane i takes chunk i % CPR of row i / CPR (+ 64 / CPR
@@ -607,17 +639,25 @@ void prefill_kernel(PrefillParams p) {
   }
 }
 
-template <int D, bool CAUSAL, bool VARLEN>
+template <int D, bool CAUSAL, bool VARLEN, bool BF16>
 int launch(const PrefillParams& p, dim3 grid, hipStream_t st) {
   KernelTimer timer;
-  timer.launch(prefill_kernel<D, CAUSAL, VARLEN>, grid, dim3(kPThreads), 0, st, p);
+  timer.launch(prefill_kernel<D, CAUSAL, VARLEN, BF16>, grid, dim3(kPThreads), 0, st, p);
   return check_launch("prefill_kernel");
 }
 
+template <int D, bool BF16>
+int launch_dt(bool causal, bool varlen, const PrefillParams& p, dim3 grid, hipStream_t st) {
+  if (causal)
+    return varlen ? launch<D, true, true, BF16>(p, grid, st) : launch<D, true, false, BF16>(p, grid, st);
+  return varlen ? launch<D, false, true, BF16>(p, grid, st) : launch<D, false, false, BF16>(p, grid, st);
+}
+
 template <int D>
-int launch_d(bool causal, bool varlen, const PrefillParams& p, dim3 grid, hipStream_t st) {
-  if (causal) return varlen ? launch<D, true, true>(p, grid, st) : launch<D, true, false>(p, grid, st);
-  return varlen ? launch<D, false, true>(p, grid, st) : launch<D, false, false>(p, grid, st);
+int launch_d(bool bf16, bool causal, bool varlen, const PrefillParams& p, dim3 grid,
+             hipStream_t st) {
+  return bf16 ? launch_dt<D, true>(causal, varlen, p, grid, st)
+              : launch_dt<D, false>(causal, varlen, p, grid, st);
 }
 
 }  // namespace
@@ -630,8 +670,10 @@ int prefill_impl(const void* q, const void* k, const void* v, void* o, float* ls
                  int64_t num_q_heads, int64_t num_kv_heads, int64_t seq_len, int64_t head_dim,
                  const int64_t q_stride[4], const int64_t k_stride[4], const int64_t v_stride[4],
                  const int64_t o_stride[4], const int64_t* lse_stride, float softmax_scale,
-                 int causal, const void* varlen, int varlen_bits, void* stream) {
+                 int causal, const void* varlen, int varlen_bits, int dtype, void* stream) {
   clear_error();
+  AKT_CHECK(dtype == AKT_DTYPE_F16 || dtype == AKT_DTYPE_BF16,
+            "prefill dtype must be AKT_DTYPE_F16 or AKT_DTYPE_BF16, got %d", dtype);
   AKT_CHECK(batch >= 0 && num_q_heads > 0 && num_kv_heads > 0, "batch/head counts must be positive");
   AKT_CHECK(num_q_heads % num_kv_heads == 0,
             "num_q_heads (%lld) must be a multiple of num_kv_heads (%lld)", (long long)num_q_heads,
@@ -690,10 +732,11 @@ int prefill_impl(const void* q, const void* k, const void* v, void* o, float* ls
   const bool is_causal = causal != 0;
   const bool is_var = varlen != nullptr;
   hipStream_t st = (hipStream_t)stream;
-  if (head_dim == 64) return launch_d<64>(is_causal, is_var, p, grid, st);
-  if (head_dim == 128) return launch_d<128>(is_causal, is_var, p, grid, st);
-  if (head_dim == 192) return launch_d<192>(is_causal, is_var, p, grid, st);
-  return launch_d<256>(is_causal, is_var, p, grid, st);
+  const bool bf16 = dtype == AKT_DTYPE_BF16;
+  if (head_dim == 64) return launch_d<64>(bf16, is_causal, is_var, p, grid, st);
+  if (head_dim == 128) return launch_d<128>(bf16, is_causal, is_var, p, grid, st);
+  if (head_dim == 192) return launch_d<192>(bf16, is_causal, is_var, p, grid, st);
+  return launch_d<256>(bf16, is_causal, is_var, p, grid, st);
 }
 }  // namespace
 
@@ -705,7 +748,7 @@ extern "C" int akt_prefill_fwd(const void* q, const void* k, const void* v, void
                                const void* varlen, int varlen_bits, void* stream) {
   return prefill_impl(q, k, v, o, nullptr, batch, num_q_heads, num_kv_heads, seq_len, head_dim,
                       q_stride, k_stride, v_stride, o_stride, nullptr, softmax_scale, causal,
-                      varlen, varlen_bits, stream);
+                      varlen, varlen_bits, AKT_DTYPE_F16, stream);
 }
 
 extern "C" int akt_prefill_fwd_lse(const void* q, const void* k, const void* v, void* o,
@@ -721,5 +764,17 @@ extern "C" int akt_prefill_fwd_lse(const void* q, const void* k, const void* v, 
   }
   return prefill_impl(q, k, v, o, lse, batch, num_q_heads, num_kv_heads, seq_len, head_dim,
                       q_stride, k_stride, v_stride, o_stride, lse_stride, softmax_scale, causal,
-                      varlen, varlen_bits, stream);
+                      varlen, varlen_bits, AKT_DTYPE_F16, stream);
+}
+
+extern "C" int akt_prefill_fwd_ex(const void* q, const void* k, const void* v, void* o,
+                                  float* lse, int64_t batch, int64_t num_q_heads,
+                                  int64_t num_kv_heads, int64_t seq_len, int64_t head_dim,
+                                  const int64_t q_stride[4], const int64_t k_stride[4],
+                                  const int64_t v_stride[4], const int64_t o_stride[4],
+                                  const int64_t lse_stride[3], float softmax_scale, int causal,
+                                  const void* varlen, int varlen_bits, int dtype, void* stream) {
+  return prefill_impl(q, k, v, o, lse, batch, num_q_heads, num_kv_heads, seq_len, head_dim,
+                      q_stride, k_stride, v_stride, o_stride, lse ? lse_stride : nullptr,
+                      softmax_scale, causal, varlen, varlen_bits, dtype, stream);
 }

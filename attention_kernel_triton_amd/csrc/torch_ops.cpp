@@ -52,17 +52,31 @@ void same_device(const char* name, const at::Tensor& t, const at::Device& dev) {
     throw py::value_error(std::string(name) + " is on " + dev_str(t) + ", expected " + dev.str());
 }
 
-// fp16 tensor with unit innermost stride and 16-byte aligned rows (a
-// contiguous copy otherwise).
+// Tensor of 2-byte elements with unit innermost stride and 16-byte aligned
+// rows (a contiguous copy otherwise).
+at::Tensor rows16(const at::Tensor& t) {
+  bool ok = t.dim() >= 1 && t.stride(-1) == 1 &&
+            (reinterpret_cast<uintptr_t>(t.data_ptr()) % 16) == 0;
+  for (int64_t i = 0; ok && i + 1 < t.dim(); ++i) ok = (t.stride(i) * 2) % 16 == 0;
+  return ok ? t : t.contiguous();
+}
+
+// fp16 tensor, as rows16.
 at::Tensor half_rows(const char* name, const at::Tensor& t) {
   need_gpu(name, t);
   if (t.scalar_type() != at::kHalf)
     throw py::type_error(std::string(name) + " must be float16, got " +
                          std::string(c10::toString(t.scalar_type())));
-  bool ok = t.dim() >= 1 && t.stride(-1) == 1 &&
-            (reinterpret_cast<uintptr_t>(t.data_ptr()) % 16) == 0;
-  for (int64_t i = 0; ok && i + 1 < t.dim(); ++i) ok = (t.stride(i) * 2) % 16 == 0;
-  return ok ? t : t.contiguous();
+  return rows16(t);
+}
+
+// fp16 or bf16 tensor of the given type, as rows16.
+at::Tensor half_or_bf16_rows(const char* name, const at::Tensor& t, at::ScalarType want) {
+  need_gpu(name, t);
+  if (t.scalar_type() != want)
+    throw py::type_error(std::string(name) + " must be " + std::string(c10::toString(want)) +
+                         " like Q, got " + std::string(c10::toString(t.scalar_type())));
+  return rows16(t);
 }
 
 at::Tensor int32_on(const char* name, const at::Tensor& t, const at::Device& dev) {
@@ -121,11 +135,16 @@ py::object result(const at::Tensor& o, const at::Tensor& lse, bool return_lse) {
 py::object prefill(const at::Tensor& Q_, const at::Tensor& K_, const at::Tensor& V_, bool causal,
                    double softmax_scale, const c10::optional<at::Tensor>& varlen_,
                    bool return_lse) {
-  at::Tensor Q = half_rows("Q", Q_), K = half_rows("K", K_), V = half_rows("V", V_);
+  need_gpu("Q", Q_);
+  const at::ScalarType dt = Q_.scalar_type();
+  if (dt != at::kHalf && dt != at::kBFloat16)
+    throw py::type_error("Q must be float16 or bfloat16, got " + std::string(c10::toString(dt)));
+  at::Tensor Q = rows16(Q_), K = half_or_bf16_rows("K", K_, dt), V = half_or_bf16_rows("V", V_, dt);
   const at::Device dev = Q.device();
   same_device("K", K, dev);
   same_device("V", V, dev);
   if (Q.dim() != 4 || K.dim() != 4) throw py::value_error("Q, K and V must be 4-D");
+  const int dtype = dt == at::kBFloat16 ? AKT_DTYPE_BF16 : AKT_DTYPE_F16;
   const int64_t B = Q.size(0), H = Q.size(1), S = Q.size(2), D = Q.size(3);
   const DeviceGuard guard(dev);
   at::Tensor O = at::empty({B, H, S, D}, Q.options());
@@ -147,19 +166,17 @@ py::object prefill(const at::Tensor& Q_, const at::Tensor& K_, const at::Tensor&
   }
   const Strides qs = strides_of(Q), ks = strides_of(K), vs = strides_of(V), os = strides_of(O);
   hipStream_t st = stream_of(Q);
+  at::Tensor lse;
+  Strides ls;
   if (return_lse) {
-    at::Tensor lse = at::empty({B, H, S}, Q.options().dtype(at::kFloat));
-    const Strides ls = strides_of(lse);
-    check_rc(akt_prefill_fwd_lse(ptr(Q), ptr(K), ptr(V), ptr(O), (float*)ptr(lse), B, H,
-                                 K.size(1), S, D, qs.v, ks.v, vs.v, os.v, ls.v,
-                                 (float)softmax_scale, causal ? 1 : 0, vptr, vbits, st),
-             "akt_prefill_fwd_lse");
-    return py::make_tuple(O, lse);
+    lse = at::empty({B, H, S}, Q.options().dtype(at::kFloat));
+    ls = strides_of(lse);
   }
-  check_rc(akt_prefill_fwd(ptr(Q), ptr(K), ptr(V), ptr(O), B, H, K.size(1), S, D, qs.v, ks.v,
-                           vs.v, os.v, (float)softmax_scale, causal ? 1 : 0, vptr, vbits, st),
-           "akt_prefill_fwd");
-  return py::cast(O);
+  check_rc(akt_prefill_fwd_ex(ptr(Q), ptr(K), ptr(V), ptr(O), (float*)ptr(lse), B, H, K.size(1),
+                              S, D, qs.v, ks.v, vs.v, os.v, return_lse ? ls.v : nullptr,
+                              (float)softmax_scale, causal ? 1 : 0, vptr, vbits, dtype, st),
+           "akt_prefill_fwd_ex");
+  return result(O, lse, return_lse);
 }
 
 // --------------------------------------------------------------------------- dense decode

@@ -7,8 +7,11 @@ signature (magicpig_..._with_norm.py:166-209) and its MagicPIG score
   u_i = 1 - (1 - p_i^K)^L - L p_i^K (1 - p_i^K)^(L-1),
   p_i = 1 - arccos(q.k_i / (|q| |k_i| + 1e-8)) / pi,
 with the reference's clamps, and per-(batch, q head) K, L (fp32 [B, Hq]).
-u_i is evaluated in fp64 because the formula cancels catastrophically for
-L near 1.  The reference returns only O; this build also returns the
+u_i is evaluated in fp32 in a cancellation-free form: for x = p_i^K >= 0.05,
+u = -expm1((L - 1) log1p(-x) + log1p((L - 1) x)); below, the series
+sum_{k>=2} (k - 1) C(L, k) (-x)^k.  (The direct formula cancels
+catastrophically when x is small or L is near 1.)  The reference returns
+only O; this build also returns the
 normaliser when ``return_lse=True``: lse[b, h] = ln sum_i exp(score_i) (fp32).
 A head with nnz == 0 yields zeros (as the reference, magicpig:51-53) and
 lse = -inf.

@@ -2,7 +2,7 @@
 
 ``flash_attention_prefill`` keeps the reference signature, asserts and output
 allocation (prefill_flash_attention.py:342-383); the work runs in the gfx950
-MFMA kernel ``akt_prefill_fwd`` (csrc/prefill.hip).  The reference's tile-size
+MFMA kernel ``akt_prefill_fwd_ex`` (csrc/prefill.hip).  The reference's tile-size
 environment variables (VAR_Q_SEQ_BLK_SIZE, VAR_KV_SEQ_BLK_SIZE) are accepted
 and ignored: results never depend on them.
 """
@@ -15,7 +15,8 @@ def flash_attention_prefill(Q, K, V, causal, softmax_scale, GQA_group_size=1, *,
                             return_lse=False):
     """O = softmax(softmax_scale * Q K^T [+ causal mask]) V.
 
-    Q: [B, H, S, D]; K, V: [B, H // GQA_group_size, S, D]; fp16 on a ROCm GPU.
+    Q: [B, H, S, D]; K, V: [B, H // GQA_group_size, S, D]; fp16 on a ROCm GPU
+    (the reference's type), or all three bf16 (bf16 MFMA, P rounded to bf16).
     Query head h attends kv head h // GQA_group_size (prefill_flash_attention.py:185).
     Returns O: [B, H, S, D] in Q's dtype; with the opt-in return_lse=True, the
     pair (O, LSE) where LSE [B, H, S] fp32 = ln sum_k exp(softmax_scale * q.k)

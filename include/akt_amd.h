@@ -15,8 +15,9 @@
  * reused by any decode entry point, but only by calls ordered on one stream
  * (calls that overlap in time must use different workspaces).
  *
- * Tensor element types: q/k/v/o and KV pools are IEEE fp16; page tables,
- * kept-token indices and counts are int32; MagicPIG K/L and LSE are fp32.
+ * Tensor element types: q/k/v/o and KV pools are IEEE fp16 (akt_prefill_fwd_ex
+ * also takes bf16); page tables, kept-token indices and counts are int32;
+ * MagicPIG K/L and LSE are fp32.
  * Strides are in elements.  The innermost (head_dim) stride must be 1 and
  * every row must start 16-byte aligned.
  *
@@ -55,6 +56,7 @@ extern "C" {
 /* Element types for entry points that accept more than one. */
 #define AKT_DTYPE_F16 0
 #define AKT_DTYPE_F32 1
+#define AKT_DTYPE_BF16 2
 
 /* Message describing the last failure on the calling thread ("" if none). */
 const char* akt_last_error(void);
@@ -73,7 +75,7 @@ int akt_abi_version(void);
  *   blocks of 64 rows that start at or beyond a sequence's length are not
  *   written (as in the reference); rows < length never read keys >= length
  *   when causal.
- *   head_dim: 64 or 128.
+ *   head_dim: 64, 128, 192 or 256.
  */
 int akt_prefill_fwd(const void* q, const void* k, const void* v, void* o,
                     int64_t batch, int64_t num_q_heads, int64_t num_kv_heads,
@@ -99,6 +101,23 @@ int akt_prefill_fwd_lse(const void* q, const void* k, const void* v, void* o, fl
                         const int64_t v_stride[4], const int64_t o_stride[4],
                         const int64_t lse_stride[3], float softmax_scale, int causal,
                         const void* varlen, int varlen_bits, void* stream);
+
+/*
+ * akt_prefill_fwd / akt_prefill_fwd_lse for either element type: q, k, v and
+ * o are all fp16 (dtype AKT_DTYPE_F16) or all bf16 (AKT_DTYPE_BF16); lse may
+ * be NULL (no normaliser; lse_stride is then ignored).  With bf16 both MFMA
+ * products run in bf16 and the probabilities are rounded to bf16 for P.V (the
+ * fp16 path rounds them to fp16, as the reference's prefill does at
+ * prefill_flash_attention.py:94).  The reference's prefill kernels take fp16
+ * only (their P.V casts P to fp16); this entry point has no counterpart there.
+ */
+int akt_prefill_fwd_ex(const void* q, const void* k, const void* v, void* o, float* lse,
+                       int64_t batch, int64_t num_q_heads, int64_t num_kv_heads,
+                       int64_t seq_len, int64_t head_dim,
+                       const int64_t q_stride[4], const int64_t k_stride[4],
+                       const int64_t v_stride[4], const int64_t o_stride[4],
+                       const int64_t lse_stride[3], float softmax_scale, int causal,
+                       const void* varlen, int varlen_bits, int dtype, void* stream);
 
 /*
  * Merge attention states computed over disjoint key sets.  For each of

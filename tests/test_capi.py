@@ -173,6 +173,18 @@ def test_prefill_lse_requires_output():
     assert rc == 1 and b"lse" in lib.akt_last_error()
 
 
+def test_prefill_ex_checks_dtype_and_allows_no_lse():
+    lib = N.load()
+    s = _i64(64 * 64, 64, 64, 1)
+    rc = lib.akt_prefill_fwd_ex(None, None, None, None, None, 1, 4, 4, 4, 64, s, s, s, s, None,
+                                0.1, 1, None, 0, 1, None)  # AKT_DTYPE_F32: not a prefill type
+    assert rc == 1 and b"dtype" in lib.akt_last_error()
+    for dtype in (0, 2):  # fp16, bf16: an empty batch launches nothing
+        rc = lib.akt_prefill_fwd_ex(None, None, None, None, None, 0, 4, 4, 4, 64, s, s, s, s,
+                                    None, 0.1, 1, None, 0, dtype, None)
+        assert rc == 0, lib.akt_last_error()
+
+
 def test_csr_entry_points_require_row_pointer():
     lib = N.load()
     s = _i64(4 * 64, 64, 64, 1)

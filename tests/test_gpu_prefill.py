@@ -32,6 +32,53 @@ def test_prefill_small_shapes(dev, D, causal, S):
     assert_close(out, ref, what=f"prefill D={D} causal={causal} S={S}")
 
 
+# bf16 bar: the output is rounded to bf16 (8 significant bits; |O| reaches
+# about 2 here, where one bf16 ulp is 2^-6) and P is rounded to bf16 for P.V.
+ATOL_BF16 = 1.6e-2
+
+
+@pytest.mark.parametrize("D", [64, 128, 192, 256])
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("S", [17, 130])
+def test_prefill_bf16_matches_oracle(dev, D, causal, S):
+    B, Hq, Hkv = 2, 4, 2
+    g = torch.Generator().manual_seed(S * 3 + D)
+    Q, K, V = (torch.randn(*sh, generator=g).bfloat16()
+               for sh in ((B, Hq, S, D), (B, Hkv, S, D), (B, Hkv, S, D)))
+    scale = 1 / math.sqrt(D)
+    out, lse = pre.flash_attention_prefill(Q.to(dev), K.to(dev), V.to(dev), causal, scale,
+                                           Hq // Hkv, return_lse=True)
+    ref, rlse = naive.prefill(Q, K, V, causal, scale, Hq // Hkv, return_lse=True)
+    assert out.dtype == torch.bfloat16 and lse.dtype == torch.float32
+    err = assert_close(out, ref, atol=ATOL_BF16, what=f"bf16 D={D} causal={causal} S={S}")
+    # The bf16 output is the fp64 result rounded: its mean error stays far
+    # below the bound (a wrong operand type or layout is off by O(1)).
+    mean = (out.float().cpu().double() - ref).abs().mean().item()
+    assert mean < 2e-3, f"mean abs err {mean:.2e} (max {err:.2e})"
+    assert_close(lse, rlse, atol=1e-2, what=f"bf16 lse D={D}")
+
+
+def test_prefill_bf16_varlen_config1_shape(dev):
+    c = syn.prefill_config(1)
+    Q, K, V = (t[:2].bfloat16() for t in (c.Q, c.K, c.V))
+    vl = c.varlen[:2]
+    out = prevar.flash_attention_prefill(Q.to(dev), K.to(dev), V.to(dev), True, c.scale, c.group,
+                                         varlen=vl.to(dev))
+    ref = naive.prefill_varlen(Q, K, V, True, c.scale, c.group, vl, dtype=torch.float32)
+    S = Q.shape[2]
+    valid = (torch.arange(S)[None, :] < vl[:, None])[:, None, :, None].expand(Q.shape)
+    assert_close(out, ref, atol=ATOL_BF16, what="bf16 var-len", mask=valid)
+
+
+def test_prefill_rejects_mixed_dtypes(dev):
+    Q, K, V = _qkv(1, 1, 2, 2, 16, 64)
+    with pytest.raises(TypeError):
+        pre.flash_attention_prefill(Q.to(dev).bfloat16(), K.to(dev), V.to(dev), True, 0.1, 1)
+    with pytest.raises(TypeError):
+        pre.flash_attention_prefill(Q.to(dev).float(), K.to(dev).float(), V.to(dev).float(),
+                                    True, 0.1, 1)
+
+
 @pytest.mark.parametrize("G", [1, 8])
 def test_prefill_group_sizes_and_unmapped_xcd_layout(dev, G):
     B, Hkv, S, D = 3, 1, 200, 64  # B*Hkv not a multiple of 8: linear block order
