@@ -11,7 +11,10 @@ Headline metric: paged decode HBM GB/s + prefill TFLOP/s.
              the LSE merge, the paged-KV append and kept-index selection).
 
 A step is one call of the drop-in entry point on the synthetic batch, and every
-entry point runs exactly one kernel.  Each leg does W untimed warm-up steps,
+entry point runs exactly one kernel.  Each leg first repeats its step, untimed,
+for --settle-ms of wall time (MI355X's clocks ramp up over tens of
+milliseconds of sustained load: config 0's prefill runs 115 us per step after
+10 cold steps and 95 us once settled), then does W untimed warm-up steps,
 then times K steps bracketed by torch.cuda.synchronize(): ms_per_step is the
 wall clock over them, and roofline.kernel_us is the GPU time of the same K
 launches from a HIP event pair recorded on the launch stream around them (so
@@ -41,19 +44,22 @@ MALL_BYTES = 256 << 20
 PROFILES = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles")
 
 
-def _traffic(summary):
+def _traffic(summary, key=None):
     """HBM bytes per launch of a kernel, from its committed counter summary.
 
     The summary records two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) of
     this script, scaled by what the counters read for a device copy of known
-    size; it holds one line ``traffic_bytes_per_launch = N``.  None if absent.
+    size; it holds a line ``traffic_bytes_per_launch = N`` (or, for a summary
+    of several legs, ``traffic_bytes_per_launch[key] = N``).  None if absent.
     """
     path = os.path.join(PROFILES, summary)
+    tag = "traffic_bytes_per_launch" + (f"[{key}]" if key else "")
     try:
         with open(path) as f:
             for line in f:
-                if line.startswith("traffic_bytes_per_launch"):
-                    return float(line.split("=")[1])
+                head, _, val = line.partition("=")
+                if head.strip() == tag:
+                    return float(val)
     except OSError:
         pass
     return None
@@ -71,6 +77,9 @@ def _parse():
                     help="all = paged (headline) + prefill + the other rows' legs; "
                          "headline = paged + prefill")
     ap.add_argument("--chunk", type=int, default=0, help="split-KV chunk tokens (0 = auto)")
+    ap.add_argument("--settle-ms", type=float, default=200.0,
+                    help="untimed repetitions of each leg's step before its warm-up steps, "
+                         "in milliseconds of wall time (0: none)")
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
                     help="also run one device-to-device copy of this many MiB "
                          "(reference kernel for HBM counter scaling)")
@@ -82,11 +91,27 @@ def _log(msg):
 
 
 # --------------------------------------------------------------------------- timing
-def _time_steps(fns, steps, warmup):
-    """(wall seconds per step, GPU seconds per step) over `steps` calls cycling
-    through fns (one kernel each), after `warmup` untimed calls."""
+def _settle(fns, seconds):
+    """Repeats the step, untimed, for `seconds` of wall time (GPU clocks ramp up
+    under sustained load); returns the number of steps run."""
+    import torch
+    n, i = len(fns), 0
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(8):
+            fns[i % n]()
+            i += 1
+        torch.cuda.synchronize()
+    return i
+
+
+def _time_steps(fns, steps, warmup, settle_s=0.0):
+    """(wall seconds per step, GPU seconds per step, settle steps) over `steps`
+    calls cycling through fns (one kernel each), after `settle_s` seconds of
+    untimed steps and then `warmup` untimed calls."""
     import torch
     n = len(fns)
+    settled = _settle(fns, settle_s) if settle_s > 0 else 0
     for i in range(warmup):
         fns[i % n]()
     torch.cuda.synchronize()
@@ -103,18 +128,20 @@ def _time_steps(fns, steps, warmup):
     gpu = e0.elapsed_time(e1) / 1e3
     if gpu > wall:  # the events are recorded inside the wall-clock window
         raise RuntimeError(f"GPU time {gpu} s exceeds the wall time {wall} s of its own steps")
-    return wall / steps, gpu / steps
+    return wall / steps, gpu / steps, settled
 
 
 def _leg(name, fns, work, unit, kernel, args, traffic=None, note=""):
     """Time a leg; work = algorithmic bytes or FLOPs per step."""
     steps = max(args.steps, len(fns))
-    t_step, t_kern = _time_steps(fns, steps, max(args.warmup, len(fns)))
+    t_step, t_kern, settled = _time_steps(fns, steps, max(args.warmup, len(fns)),
+                                          args.settle_ms / 1e3)
     scale = 1e9 if unit == "GB/s" else 1e12
     bound = "hbm" if unit == "GB/s" else "mfma"
     peak = HBM_PEAK_GBS if bound == "hbm" else FP16_PEAK_TFLOPS
     out = {"value": work / t_step / scale, "unit": unit, "ms_per_step": t_step * 1e3,
            "work_per_step": work, "steps": steps,
+           "settle": {"ms": args.settle_ms, "steps": settled},
            "roofline": {"bound": bound, "achieved": work / t_kern / scale, "peak": peak,
                         "unit": unit, "frac": work / t_kern / scale / peak, "traffic": traffic,
                         "kernel": kernel, "kernel_us": t_kern * 1e6}}
@@ -462,6 +489,10 @@ def bench_legs(args):
     legs["paged_append"]["cpu_baseline"] = _cpu_baseline(
         cpu9, 8 * nb_cpu * T * Hkv * D, "GB/s",
         f"{nb_cpu} of the {Bq} sequences (numpy, one token at a time)", budget, args)
+    # HBM bytes per launch of each leg's kernel, from the committed counter summary.
+    for key, leg in legs.items():
+        if leg["roofline"]["traffic"] is None:
+            leg["roofline"]["traffic"] = _traffic("legs_hbm_traffic.md", key)
     return legs
 
 
@@ -508,6 +539,8 @@ def main():
             res["cpu_baseline"] = cb
         pg.pop("unit", None)
         res["config"].update({"bytes_per_step": pg.pop("work_per_step"), "tokens": pg["tokens"]})
+        # Untimed steps before the W warm-up steps (GPU clocks ramp up under load).
+        res["settle"] = pg.pop("settle")
         torch.cuda.empty_cache()
     if args.only in ("all", "headline", "prefill"):
         pf = bench_prefill(args)
