@@ -7,14 +7,16 @@
 // bf16 form for bf16 tensors) and the transposing LDS read (ds_read_b64_tr_b16).
 //
 // Work decomposition.  A 256-thread workgroup serves one (batch, kv head) and
-// four "slots"; slot f = (query head f % G, 64-row block f / G) of that kv
-// head's G query heads.  With G a multiple of 4 the four waves are four query
-// heads at the same rows: they share every staged K/V tile and have identical
-// causal extents.  Each wave owns 64 query rows as two 32-row MFMA blocks that
-// share every K and V fragment read from LDS.
+// four "slots"; slot f = (query head f % G, row block f / G) of that kv head's
+// G query heads (64-row blocks at D = 64, 32-row blocks above).  With G a
+// multiple of 4 the four waves are four query heads at the same rows: they
+// share every staged K/V tile and have identical causal extents.  At D = 64 each wave owns 64 query rows as two 32-row MFMA
+// blocks that share every K and V fragment read from LDS; at larger head dims
+// one 32-row block (see rblocks_for).
 //
-// K/V staging.  Each 64-key tile of K and V goes global -> registers -> one
-// of four LDS tile buffers: while tile j is computed, tile j + 1 is already
+// K/V staging.  Each tile of K and V (64 keys at D = 64, else 32) goes
+// global -> registers -> one of four LDS tile buffers: while tile j is
+// computed, tile j + 1 is already
 // published, tile j + 2 is being written and tile j + 3 is in flight from
 // HBM, and one barrier per tile both publishes a tile and retires tile j - 2's
 // buffer.  (Direct global -> LDS copies would be waited for before every
@@ -68,11 +70,14 @@ constexpr int kPThreads = 256;
 constexpr int kSlots = 4;   // waves per workgroup
 constexpr int kNBuf = 4;    // LDS tile buffers
 // 32-row MFMA blocks per wave, query rows per slot and keys per staged tile:
-// two blocks and 64-key tiles up to D = 128; at D = 192 and 256 one block (the
-// register budget) and 32-key tiles (four K + V buffers then fit in 128 KB).
-__host__ __device__ constexpr int rblocks_for(int D) { return D >= 192 ? 1 : 2; }
+// two blocks and 64-key tiles at D = 64 (two waves per SIMD in 237 VGPRs);
+// from D = 128 one block and 32-key tiles.  At D = 128 that holds a wave in
+// 210 VGPRs and a workgroup's four K + V buffers in 64 KB, so two waves share
+// each SIMD (two blocks took 509 registers: one wave per SIMD, 4% slower); at
+// D = 192 and 256 the register budget allows one wave per SIMD either way.
+__host__ __device__ constexpr int rblocks_for(int D) { return D >= 128 ? 1 : 2; }
 __host__ __device__ constexpr int rows_for(int D) { return 32 * rblocks_for(D); }
-__host__ __device__ constexpr int tile_keys_for(int D) { return D >= 192 ? 32 : 64; }
+__host__ __device__ constexpr int tile_keys_for(int D) { return D >= 128 ? 32 : 64; }
 constexpr float kRescaleSlack = 8.0f;
 // Largest row sum of one 32-key step that lets P stay unchecked: below it
 // every probability is under 32 * 2^kRescaleSlack, far inside fp16's range;
@@ -188,7 +193,7 @@ __device__ __forceinline__ int div_small(int n, int d, float inv) {
 }
 
 template <int D, bool CAUSAL, bool VARLEN, bool BF16>
-__global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(D == 64 ? 2 : 1, 2)))
+__global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 2 : 1, 2)))
 void prefill_kernel(PrefillParams p) {
   typedef Elt<BF16> E;
   typedef typename E::v8 v8;
