@@ -190,8 +190,9 @@ struct IssueCtx {
   int page_pref, slot_pref;  // aligned paged: page id / slot of this wave's k-th group (lane k)
 };
 
-// PERSIST: the grid is sized to the machine and each workgroup walks items
-// blockIdx.x, blockIdx.x + gridDim.x, ... (dense and paged caches).  For a
+// PERSIST: the grid is sized to the machine and each workgroup starts with
+// item blockIdx.x and takes the rest from a ticket counter (dense and paged
+// caches; see the driver below).  For a
 // paged cache the per-sequence chunk prefix is built once per workgroup in
 // LDS, so resolving an item needs no global loads.  Each wave streams its
 // groups continuously across items: the last two groups of an item are
@@ -235,6 +236,7 @@ __attribute__((amdgpu_waves_per_eu(split_min_waves<D, GT>(), 8))) void split_ker
   __shared__ int sm_ps[TABLE ? kMaxTableB : 1];
   __shared__ int sm_wtot[kWaves];
   __shared__ int sm_next;
+  __shared__ int sm_seq;  // items whose ticket thread 0 has published in sm_next
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -835,6 +837,9 @@ __attribute__((amdgpu_waves_per_eu(split_min_waves<D, GT>(), 8))) void split_ker
   // ---- drivers ---------------------------------------------------------------
   if constexpr (PERSIST) {
     int n_items;
+    // LDS starts with whatever the CU's previous workgroup left: sm_seq
+    // must read 0 before any wave can compare it (barriers below).
+    if (tid == 0) sm_seq = 0;
     if constexpr (TABLE) {
       // Chunk prefix over sequences (block-wide exclusive scan), once.
       int carry = 0;
@@ -876,6 +881,7 @@ __attribute__((amdgpu_waves_per_eu(split_min_waves<D, GT>(), 8))) void split_ker
         if (sm_len[bb] == 0) zero_sequence(bb);
     } else {
       n_items = p.B * ((p.S + p.chunk - 1) / p.chunk) * Y;
+      __syncthreads();  // sm_seq
     }
     // The item whose first groups the current item's last iterations
     // prefetch.  Past the last item it is the current one with an empty
@@ -887,14 +893,27 @@ __attribute__((amdgpu_waves_per_eu(split_min_waves<D, GT>(), 8))) void split_ker
       w.t1 = w.t0;
       return w;
     };
-    // Dynamic schedule: workgroup w starts with items w and w + gridDim.x,
-    // then takes tickets 2 * gridDim.x, 2 * gridDim.x + 1, ... from
-    // counters[0], two items ahead so the atomic's latency is hidden (and
-    // the first two items need no atomic at all).  The last workgroup to
-    // exit resets both counters to zero for the next launch.
+    // Dynamic schedule: workgroup w starts with item w, then takes tickets
+    // from counters[0] (item gridDim.x + ticket); the last workgroup to exit
+    // resets both counters to zero for the next launch.
+    // - Long items (NEAR, GPW >= 6): the ticket thread 0 takes after group
+    //   kAtomicK names the next item.  Thread 0 publishes it in LDS after
+    //   group kPublishK (sm_next, then the item count in sm_seq) and every
+    //   wave sets the next item up after group kTicketK, in time for the
+    //   prefetch of its first groups.  When the tickets run out a workgroup
+    //   has at most the rest of its current item and one more left, so the
+    //   last workgroups to finish trail the mean by about one item.
+    // - Short items: the ticket names the item after next (items w and
+    //   w + gridDim.x start the walk), read back at the workgroup merge, so
+    //   the atomic's latency stays hidden even in a two-group item.
+    constexpr bool NEAR = GPW >= 6;
+    constexpr int kTicketK = GPW - 4;                     // next item set up
+    constexpr int kPublishK = kTicketK - 1;               // ticket in LDS
+    constexpr int kAtomicK = kPublishK >= 3 ? kPublishK - 2 : 0;  // ticket taken
     int i = blockIdx.x;
     int nxt = i + (int)gridDim.x;
     int ticket_raw = 0;  // thread 0: counters[0] before its increment
+    int seq = 0;         // items this workgroup has begun
     if (i < n_items) {  // workgroup-uniform; the grid is sized from an upper bound
     Item nx;
     IssueCtx cc, nc;
@@ -902,22 +921,50 @@ __attribute__((amdgpu_waves_per_eu(split_min_waves<D, GT>(), 8))) void split_ker
     it = resolve_persistent(i);
     make_uniform(it);
     setup(it, cc, qf);
-    nx = resolve_next(nxt, i);
-    make_uniform(nx);
-    setup(nx, nc, qn);
+    if constexpr (!NEAR) {
+      nx = resolve_next(nxt, i);
+      make_uniform(nx);
+      setup(nx, nc, qn);
+    }
     Buf bufs[2];
     issue(cc, cc.g_begin + wave, bufs[0]);
     issue(cc, cc.g_begin + wave + kWaves, bufs[1]);
     for (;;) {
-      // The returned value is first used at the item's end (adding the offset
-      // here would make the wave wait for the loads in flight at once).
-      if (tid == 0) ticket_raw = atomicAdd(&p.counters[0], 1);
+      // The returned value is first used two groups later (NEAR) or at the
+      // item's end: using it at once would make the wave wait for the loads
+      // in flight.
+      if constexpr (!NEAR) {
+        if (tid == 0) ticket_raw = atomicAdd(&p.counters[0], 1);
+      }
       begin_item();
+      ++seq;
       // Groups k of this item; the prefetch two groups ahead crosses into the
       // next item for the last two (k + 2 >= GPW is a compile-time condition).
 #pragma unroll
       for (int k = 0; k < GPW; ++k) {
         consume(bufs[k & 1]);
+        if constexpr (NEAR) {
+          if (k == kAtomicK && tid == 0) ticket_raw = atomicAdd(&p.counters[0], 1);
+          if (k == kPublishK && tid == 0) {
+            // Waiting for the ticket waits for the loads issued before the
+            // atomic (groups up to kAtomicK + 1, all consumed) and no others.
+            // The two volatile stores stay in program order, and LDS serves
+            // one wave's operations in order.
+            *(volatile int*)&sm_next = (int)gridDim.x + ticket_raw;
+            *(volatile int*)&sm_seq = seq;
+          }
+          if (k == kTicketK) {
+            // Thread 0 wrote this item's ticket after group kPublishK; a
+            // wave this far ahead of wave 0 waits for it.  The previous item's
+            // reads of sm_next all precede the workgroup merge's barrier,
+            // which precedes thread 0's next write.
+            while (*(volatile int*)&sm_seq != seq) __builtin_amdgcn_s_sleep(1);
+            nxt = uniform(*(volatile int*)&sm_next);
+            nx = resolve_next(nxt, i);
+            make_uniform(nx);
+            setup(nx, nc, qn);
+          }
+        }
         if constexpr (DEFER) {
           if (k == 2 && has_pend && tid == 0) {
             // Group 2's loads were issued after the pending partial's stores
@@ -934,21 +981,25 @@ __attribute__((amdgpu_waves_per_eu(split_min_waves<D, GT>(), 8))) void split_ker
         else issue(nc, nc.g_begin + wave + kWaves * (k + 2 - GPW), bufs[k & 1]);
       }
       if (tid == 0) {  // read back by finish() after its first barrier
-        sm_next = 2 * (int)gridDim.x + ticket_raw;
+        // (NEAR: a wave behind wave 0 may still have to read this item's
+        // ticket from sm_next, so it is not rewritten here.)
+        if constexpr (!NEAR) sm_next = 2 * (int)gridDim.x + ticket_raw;
         if constexpr (DEFER) sm_pflag = has_pend && arr == sm_pend.nch - 1;
       }
       const int ticket = finish();
       const int inext = nxt;
-      nxt = ticket;
+      if constexpr (!NEAR) nxt = ticket;
       if (inext >= n_items) break;  // the last prefetch read q rows (see resolve_next)
       i = inext;
       it = nx;
       cc = nc;
 #pragma unroll
       for (int s = 0; s < KS; ++s) qf[s] = qn[s];
-      nx = resolve_next(nxt, i);
-      make_uniform(nx);
-      setup(nx, nc, qn);
+      if constexpr (!NEAR) {
+        nx = resolve_next(nxt, i);
+        make_uniform(nx);
+        setup(nx, nc, qn);
+      }
     }
     }  // i < n_items
     if constexpr (DEFER) {
