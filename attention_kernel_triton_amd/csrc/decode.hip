@@ -1249,15 +1249,20 @@ int64_t paged_chunk(int64_t chunk_tokens, int64_t total_pages, int64_t page_size
 }
 
 // Automatic split count of sparse rows: as many splits per row as fit one
-// round of resident workgroups, at most one per 64 index slots.  A sparse
-// workgroup is a chain of dependent round trips (nnz, page table, indices,
-// page ids, rows) whatever its token count, so a second round of workgroups
-// costs a whole second chain.  Measured on MI355X (split kernel):
-//   config 4a (32 rows):  32 splits 10.5-11.0 us, 16 splits 6.9-7.9 us;
-//   config 4b (96 rows):  11 splits 20.3-20.5 us, 5 splits 16.8 us;
-//   MagicPIG 4b:          11 splits 26.6 us,      5 splits 23.8 us.
+// round of resident workgroups, at most kMaxAutoSplits and at most one per 64
+// index slots.  A sparse workgroup is a chain of dependent round trips (nnz,
+// page table, indices, page ids, rows) whatever its token count, so a second
+// round of workgroups costs a whole second chain, and a split of a few
+// groups pays the chain for little streaming.  Measured on MI355X (split
+// kernel, settled, rotated inputs):
+//   config 4a (32 rows):  32 splits 16.4 us, 16 splits 9.8 us, 12 / 8 / 4
+//                         splits 9.1 / 9.2 / 9.1 us, 2 splits 11.4 us;
+//   config 4b (96 rows):  11 splits 23.8 us, 8 splits 29.1 us, 5 splits
+//                         18.7 us, 4 splits 19.3 us, 2 splits 20.4 us.
+constexpr int64_t kMaxAutoSplits = 8;
 int64_t auto_splits(int64_t rows, int64_t l_max) {
   int64_t s = kResidentWorkgroups / (rows > 0 ? rows : 1);
+  if (s > kMaxAutoSplits) s = kMaxAutoSplits;
   const int64_t cap = ceil_div(l_max > 0 ? l_max : 1, 64);
   if (s > cap) s = cap;
   return s < 1 ? 1 : s;

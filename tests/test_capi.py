@@ -123,11 +123,13 @@ def test_automatic_chunk_length():
 
 def test_automatic_sparse_split_count():
     """Sparse rows get as many splits as fit one round of ~512 resident workgroups,
-    at most one per 64 index slots of l_max; the workspace size shows the count."""
+    at most 8 and at most one per 64 index slots of l_max; the workspace size shows
+    the count."""
     lib = N.load()
     ws = lib.akt_sparse_decode_workspace_size
     part = lambda rows, ns, D: _ws(rows, rows * ns if ns > 1 else 0, 1, D)  # noqa: E731
-    assert ws(1, 32, 128, 3840, 0) == part(32, 16, 128)      # config 4a: 512 / 32 rows
+    assert ws(1, 32, 128, 3840, 0) == part(32, 8, 128)       # config 4a: 512 / 32 rows, capped at 8
+    assert ws(1, 64, 128, 3840, 0) == part(64, 8, 128)       # 512 / 64 rows
     assert ws(3, 32, 256, 32768, 0) == part(96, 5, 256)      # config 4b: 512 / 96 rows
     assert ws(1, 32, 128, 200, 0) == part(32, 4, 128)        # capped at ceil(200 / 64)
     assert ws(64, 32, 128, 3840, 0) == part(2048, 1, 128)    # 2048 rows: one split, no partials
