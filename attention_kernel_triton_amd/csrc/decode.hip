@@ -609,9 +609,15 @@ __attribute__((amdgpu_waves_per_eu(split_min_waves<D, GT>(), 8))) void split_ker
 
   // ---- output of a unit ----------------------------------------------------
   constexpr int NV = GT * D / 4;  // float4 vectors of a unit's output (head-major)
+  // Groups in flight per wave in the persistent loop: 4 for dense D = 64
+  // (a group's buffer is 17 registers, and a workgroup streams a single
+  // item there, so the loads of a deeper window shorten its dependent chain),
+  // else 2.
+  constexpr int PD = (PERSIST && MODE == kModeDense && D == 64 && GPW >= 5) ? 4 : 2;
   // Arrival of a stored partial is counted one item late in the persistent
-  // loop (see the driver), which needs the item's third group.
-  constexpr bool DEFER = PERSIST && GPW >= 3;
+  // loop (see the driver), which needs the item's group PD (the first whose
+  // loads the item itself issues).
+  constexpr bool DEFER = PERSIST && GPW >= PD + 1;
   // Normalised output of head h of item w, dims d0 .. d0 + 3, and (d0 == 0) its LSE.
   auto write_out = [&](const Item& w, int h, int d0, float4_t O, float M, float L, float E) {
     const int64_t row = (int64_t)w.b * p.Hq + w.hq0 + h;
@@ -906,7 +912,7 @@ __attribute__((amdgpu_waves_per_eu(split_min_waves<D, GT>(), 8))) void split_ker
     // - Short items: the ticket names the item after next (items w and
     //   w + gridDim.x start the walk), read back at the workgroup merge, so
     //   the atomic's latency stays hidden even in a two-group item.
-    constexpr bool NEAR = GPW >= 6;
+    constexpr bool NEAR = GPW >= 6 && PD == 2;
     constexpr int kTicketK = GPW - 4;                     // next item set up
     constexpr int kPublishK = kTicketK - 1;               // ticket in LDS
     constexpr int kAtomicK = kPublishK >= 3 ? kPublishK - 2 : 0;  // ticket taken
@@ -926,9 +932,9 @@ __attribute__((amdgpu_waves_per_eu(split_min_waves<D, GT>(), 8))) void split_ker
       make_uniform(nx);
       setup(nx, nc, qn);
     }
-    Buf bufs[2];
-    issue(cc, cc.g_begin + wave, bufs[0]);
-    issue(cc, cc.g_begin + wave + kWaves, bufs[1]);
+    Buf bufs[PD];
+#pragma unroll
+    for (int j = 0; j < PD; ++j) issue(cc, cc.g_begin + wave + kWaves * j, bufs[j]);
     for (;;) {
       // The returned value is first used two groups later (NEAR) or at the
       // item's end: using it at once would make the wave wait for the loads
@@ -938,11 +944,11 @@ __attribute__((amdgpu_waves_per_eu(split_min_waves<D, GT>(), 8))) void split_ker
       }
       begin_item();
       ++seq;
-      // Groups k of this item; the prefetch two groups ahead crosses into the
-      // next item for the last two (k + 2 >= GPW is a compile-time condition).
+      // Groups k of this item; the prefetch PD groups ahead crosses into the
+      // next item for the last PD (k + PD >= GPW is a compile-time condition).
 #pragma unroll
       for (int k = 0; k < GPW; ++k) {
-        consume(bufs[k & 1]);
+        consume(bufs[k % PD]);
         if constexpr (NEAR) {
           if (k == kAtomicK && tid == 0) ticket_raw = atomicAdd(&p.counters[0], 1);
           if (k == kPublishK && tid == 0) {
@@ -966,19 +972,20 @@ __attribute__((amdgpu_waves_per_eu(split_min_waves<D, GT>(), 8))) void split_ker
           }
         }
         if constexpr (DEFER) {
-          if (k == 2 && has_pend && tid == 0) {
-            // Group 2's loads were issued after the pending partial's stores
-            // (at the previous finish()), and wave 0 has just waited for
-            // them: in-order completion makes those stores complete too.
-            // The empty asm consumes a word of group 2 and yields 0, so the
-            // count cannot be issued before that wait.
+          if (k == PD && has_pend && tid == 0) {
+            // Group PD's loads, the first issued in this item, were issued
+            // after the pending partial's stores (at the previous finish()),
+            // and wave 0 has just waited for them: in-order completion makes
+            // those stores complete too.  The empty asm consumes a word of
+            // group PD and yields 0, so the count cannot be issued before
+            // that wait.
             int zero = 0;
             asm volatile("" : "+s"(zero) : "v"(bufs[0].k[0][0]));
             arr = atomicAdd(&p.arrive[sm_pend.unit + zero], 1);
           }
         }
-        if (k + 2 < GPW) issue(cc, cc.g_begin + wave + kWaves * (k + 2), bufs[k & 1]);
-        else issue(nc, nc.g_begin + wave + kWaves * (k + 2 - GPW), bufs[k & 1]);
+        if (k + PD < GPW) issue(cc, cc.g_begin + wave + kWaves * (k + PD), bufs[k % PD]);
+        else issue(nc, nc.g_begin + wave + kWaves * (k + PD - GPW), bufs[k % PD]);
       }
       if (tid == 0) {  // read back by finish() after its first barrier
         // (NEAR: a wave behind wave 0 may still have to read this item's
