@@ -13,9 +13,15 @@
 // Tokens whose position or page id falls outside the table / pool are
 // skipped, never written.
 //
-// Work: one thread per 16-byte chunk of one (token, kv head) row; a chunk of
-// K and the matching chunk of V are moved together.  HBM-bound: 4 * D bytes
-// per (token, kv head) (read K and V, write K and V).
+// Work: one wave per run of kTPW consecutive new tokens.  The wave finds the
+// sequence of each of its tokens with one ballot per 64 sequences over
+// append_indptr (the sequences are consecutive runs of rows), lane t looks
+// up token t's page and slot (two rounds of loads for all tokens at once),
+// and the lanes then move 16-byte chunks of the tokens' (kv head, dim) rows,
+// the loads of token t + 1 issued before the stores of token t.  Each lane
+// owns chunks lane + 64 j (j < NPL) of a token's Hkv * D / 8 chunks of K
+// (and the same chunks of V); rows of more chunks take several passes.
+// HBM-bound: 4 * D bytes per (token, kv head) (read K and V, write K and V).
 #include "akt_common.hpp"
 #include "akt_host.hpp"
 
@@ -23,6 +29,8 @@ namespace akt {
 namespace {
 
 constexpr int kAThreads = 256;
+constexpr int kAWaves = kAThreads / 64;
+constexpr int kTPW = 2;  // new tokens per wave (2: 54.5 us on the bench leg; 4: 55.3, 8: 56.6, 16: 63.4)
 
 struct AppendParams {
   const half_t* k_new;
@@ -38,40 +46,96 @@ struct AppendParams {
   int B, Hkv, cpr, page_size, num_pool_pages;
 };
 
+template <int NPL>
 __global__ __launch_bounds__(kAThreads) void paged_append_kernel(AppendParams p) {
-  const int64_t gt = (int64_t)blockIdx.x * kAThreads + threadIdx.x;
-  const int64_t per_tok = (int64_t)p.Hkv * p.cpr;
-  const int64_t tok = gt / per_tok;
-  if (tok >= p.total_new) return;
-  const int rem = (int)(gt - tok * per_tok);
-  const int h = rem / p.cpr;
-  const int c = rem - h * p.cpr;
-  // Sequence of new row `tok`: last b with append_indptr[b] <= tok.
-  int lo = 0, hi = p.B - 1;
-  while (lo < hi) {
-    const int mid = (lo + hi + 1) >> 1;
-    if (p.append_indptr[mid] <= tok) lo = mid;
-    else hi = mid - 1;
+  const int lane = threadIdx.x & 63;
+  const int wave = uniform(threadIdx.x >> 6);
+  const int64_t tok0 = ((int64_t)blockIdx.x * kAWaves + wave) * kTPW;
+  if (tok0 >= p.total_new) return;  // wave-uniform
+  const int nt = (int)min((int64_t)kTPW, p.total_new - tok0);
+  const int per_tok = p.Hkv * p.cpr;  // chunks of one token's K (or V) rows
+
+  // Sequence of token tok0 + t: cnt[t] - 1, where cnt[t] counts the
+  // sequences b < B with append_indptr[b] <= tok0 + t (the rows of sequence
+  // b are append_indptr[b] .. append_indptr[b + 1] - 1).
+  int cnt[kTPW];
+#pragma unroll
+  for (int t = 0; t < kTPW; ++t) cnt[t] = 0;
+  for (int jb = 0; jb < p.B; jb += 64) {  // wave-uniform
+    const int j = jb + lane;
+    const int64_t aj = j < p.B ? (int64_t)p.append_indptr[j] : INT64_MAX;
+#pragma unroll
+    for (int t = 0; t < kTPW; ++t) cnt[t] += __popcll(__ballot(aj <= tok0 + t));
   }
-  const int b = lo;
-  const int64_t a0 = p.append_indptr[b], a1 = p.append_indptr[b + 1];
-  if (tok < a0 || tok >= a1) return;  // malformed indptr: nothing to write
-  const int np = p.indptr[b + 1] - p.indptr[b];
-  if (np <= 0) return;
-  const int last = min(max(p.last_len[b], 0), p.page_size);
-  const int64_t len = (int64_t)(np - 1) * p.page_size + last;
-  const int64_t pos = len - (a1 - a0) + (tok - a0);
-  if (pos < 0 || pos >= len) return;
-  const int lp = (int)(pos / p.page_size);
-  const int slot = (int)(pos - (int64_t)lp * p.page_size);
-  const int page = p.indices[p.indptr[b] + lp];
-  if (page < 0 || page >= p.num_pool_pages) return;
-  const half_t* ks = p.k_new + tok * p.kn_st + (int64_t)h * p.kn_sh + 8 * c;
-  const half_t* vs = p.v_new + tok * p.vn_st + (int64_t)h * p.vn_sh + 8 * c;
-  half_t* dst = p.pool + (int64_t)page * p.sp + (int64_t)h * p.sh + (int64_t)slot * p.ss + 8 * c;
-  const uint4_t kv = ld16(ks), vv = ld16(vs);
-  st16(dst, kv);
-  st16(dst + p.skv, vv);
+  // Lane t < nt: token tok0 + t's page id and slot, or page -1 (skipped):
+  // the token's rows are the last ones of its sequence under the updated
+  // table, positions len - n .. len - 1.
+  int my_b = -1;
+#pragma unroll
+  for (int t = 0; t < kTPW; ++t)
+    if (lane == t) my_b = cnt[t] - 1;
+  int page = -1, slot = 0;
+  if (lane < nt && my_b >= 0) {
+    const int64_t tok = tok0 + lane;
+    const int64_t a0 = p.append_indptr[my_b], a1 = p.append_indptr[my_b + 1];
+    const int ip0 = p.indptr[my_b], ip1 = p.indptr[my_b + 1];
+    const int np = ip1 - ip0;
+    const int last = min(max(p.last_len[my_b], 0), p.page_size);
+    const int64_t len = (int64_t)(np - 1) * p.page_size + last;
+    const int64_t pos = len - (a1 - a0) + (tok - a0);
+    // A malformed indptr (the token outside its sequence's rows) or a
+    // position outside the table writes nothing.
+    if (tok >= a0 && tok < a1 && np > 0 && pos >= 0 && pos < len) {
+      const int lp = (int)(pos / p.page_size);
+      const int pg = p.indices[ip0 + lp];
+      if (pg >= 0 && pg < p.num_pool_pages) {
+        page = pg;
+        slot = (int)(pos - (int64_t)lp * p.page_size);
+      }
+    }
+  }
+
+  // This lane's chunks: (kv head, 16-byte chunk) of chunk index lane + 64 j.
+  for (int cb = 0; cb < per_tok; cb += 64 * NPL) {  // wave-uniform passes
+    int64_t ksrc[NPL], vsrc[NPL], dst_off[NPL];
+    bool has[NPL];
+#pragma unroll
+    for (int j = 0; j < NPL; ++j) {
+      const int i = cb + lane + 64 * j;
+      has[j] = i < per_tok;
+      const int h = has[j] ? i / p.cpr : 0;
+      const int c = has[j] ? i - h * p.cpr : 0;
+      ksrc[j] = (int64_t)h * p.kn_sh + 8 * c;
+      vsrc[j] = (int64_t)h * p.vn_sh + 8 * c;
+      dst_off[j] = (int64_t)h * p.sh + 8 * c;
+    }
+    uint4_t kb[2][NPL], vb[2][NPL];
+    // Rows of token tok0 + t; t past the wave's last token re-reads it.
+    auto load = [&](int t, uint4_t (&kd)[NPL], uint4_t (&vd)[NPL]) {
+      const int64_t tok = tok0 + min(t, nt - 1);
+#pragma unroll
+      for (int j = 0; j < NPL; ++j) {
+        kd[j] = has[j] ? ld16(p.k_new + tok * p.kn_st + ksrc[j]) : uint4_t{0, 0, 0, 0};
+        vd[j] = has[j] ? ld16(p.v_new + tok * p.vn_st + vsrc[j]) : uint4_t{0, 0, 0, 0};
+      }
+    };
+    load(0, kb[0], vb[0]);
+#pragma unroll
+    for (int t = 0; t < kTPW; ++t) {
+      if (t + 1 < kTPW) load(t + 1, kb[(t + 1) & 1], vb[(t + 1) & 1]);
+      const int pg = __builtin_amdgcn_readlane(page, t);
+      const int sl = __builtin_amdgcn_readlane(slot, t);
+      if (t < nt && pg >= 0) {  // wave-uniform
+        half_t* dst = p.pool + (int64_t)pg * p.sp + (int64_t)sl * p.ss;
+#pragma unroll
+        for (int j = 0; j < NPL; ++j)
+          if (has[j]) {
+            st16(dst + dst_off[j], kb[t & 1][j]);
+            st16(dst + p.skv + dst_off[j], vb[t & 1][j]);
+          }
+      }
+    }
+  }
 }
 
 }  // namespace
@@ -124,11 +188,22 @@ extern "C" int akt_paged_kv_append(const void* k_new, const void* v_new,
   p.cpr = (int)(head_dim / 8);
   p.page_size = (int)page_size;
   p.num_pool_pages = (int)(num_pool_pages < (1ll << 31) ? num_pool_pages : (1ll << 31) - 1);
-  const int64_t threads = total_new * num_kv_heads * p.cpr;
-  const int64_t grid = ceil_div(threads, kAThreads);
+  AKT_CHECK(num_kv_heads * p.cpr < (1ll << 30), "num_kv_heads * head_dim too large");
+  AKT_CHECK(batch < (1ll << 31), "batch too large");
+  const int64_t grid = ceil_div(ceil_div(total_new, kTPW), kAWaves);
   AKT_CHECK(grid < (1ll << 31), "too many tokens");
+  // Chunks per lane per pass: the fewest of 1, 2, 4, 8 that cover a token's
+  // Hkv * D / 8 chunks in one pass (rows of more than 512 chunks take several).
+  const int64_t per_tok = num_kv_heads * p.cpr;
   KernelTimer timer;
-  timer.launch(paged_append_kernel, dim3((unsigned)grid), dim3(kAThreads), 0,
-               (hipStream_t)stream, p);
+  const dim3 g((unsigned)grid), blk(kAThreads);
+  if (per_tok <= 64)
+    timer.launch(paged_append_kernel<1>, g, blk, 0, (hipStream_t)stream, p);
+  else if (per_tok <= 128)
+    timer.launch(paged_append_kernel<2>, g, blk, 0, (hipStream_t)stream, p);
+  else if (per_tok <= 256)
+    timer.launch(paged_append_kernel<4>, g, blk, 0, (hipStream_t)stream, p);
+  else
+    timer.launch(paged_append_kernel<8>, g, blk, 0, (hipStream_t)stream, p);
   return check_launch("paged_append_kernel");
 }

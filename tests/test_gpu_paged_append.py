@@ -42,6 +42,38 @@ def test_append_kernel_is_bit_exact(dev, page, D):
     assert np.array_equal(gpool.cpu().numpy(), ref)
 
 
+@pytest.mark.parametrize("B,Hkv,D,page", [(70, 2, 64, 16), (9, 3, 512, 8), (5, 5, 1024, 4)])
+def test_append_many_sequences_and_wide_rows(dev, B, Hkv, D, page):
+    """More sequences than a wave has lanes (the sequence search runs in
+    64-sequence steps), runs of new tokens of 0 to 11 rows (sequence changes
+    inside one wave's run of tokens), and token rows of 192 and 640 16-byte
+    chunks (a partial last chunk column, and two passes over a row)."""
+    rng = np.random.default_rng(B * 7 + D)
+    counts = rng.integers(0, 12, size=B)
+    counts[::5] = 0
+    hist = rng.integers(0, 40, size=B)
+    lens = hist + counts
+    P = int(sum(-(-int(n) // page) for n in lens)) + 3
+    perm = rng.permutation(P)
+    indptr, indices, last, off = [0], [], [], 0
+    for n in lens:
+        npg = -(-int(n) // page)
+        indices += [int(x) for x in perm[off:off + npg]]
+        off += npg
+        indptr.append(len(indices))
+        last.append(0 if n == 0 else (int(n) - 1) % page + 1)
+    ap = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    pool = rng.standard_normal((P, 2, Hkv, page, D)).astype(np.float16)
+    k_new = rng.standard_normal((int(ap[-1]), Hkv, D)).astype(np.float16)
+    v_new = rng.standard_normal((int(ap[-1]), Hkv, D)).astype(np.float16)
+    ref = paged_append(pool, k_new, v_new, ap, np.array(indptr), np.array(indices), np.array(last))
+    gpool = torch.from_numpy(pool).to(dev)
+    t = lambda a: torch.tensor(np.asarray(a), dtype=torch.int32, device=dev)  # noqa: E731
+    append_paged_kv(torch.from_numpy(k_new).to(dev), torch.from_numpy(v_new).to(dev), t(ap), gpool,
+                    t(indptr), t(indices), t(last))
+    assert np.array_equal(gpool.cpu().numpy(), ref)
+
+
 def test_append_strided_new_rows(dev):
     """k_new / v_new given as views of a [total, 2, Hkv, D] projection output."""
     rng = np.random.default_rng(3)
