@@ -189,7 +189,7 @@ extern "C" int akt_paged_kv_append(const void* k_new, const void* v_new,
   p.page_size = (int)page_size;
   p.num_pool_pages = (int)(num_pool_pages < (1ll << 31) ? num_pool_pages : (1ll << 31) - 1);
   AKT_CHECK(num_kv_heads * p.cpr < (1ll << 30), "num_kv_heads * head_dim too large");
-  AKT_CHECK(batch < (1ll << 31), "batch too large");
+  AKT_CHECK(batch < (1ll << 30), "batch too large");  // the kernel steps sequences by 64 in int
   const int64_t grid = ceil_div(ceil_div(total_new, kTPW), kAWaves);
   AKT_CHECK(grid < (1ll << 31), "too many tokens");
   // Chunks per lane per pass: the fewest of 1, 2, 4, 8 that cover a token's
