@@ -83,26 +83,41 @@ __global__ __launch_bounds__(kMThreads) void merge_kernel(MergeParams p) {
   if (row >= p.rows) return;
   const TI* op = static_cast<const TI*>(p.o_parts) + row * p.o_sr + d0;
   const float* lp = p.lse_parts + row * p.l_sr;
-  // Online merge in log2 units: m = running max of LSE_i * log2(e).
+  // Online merge in log2 units: m = running max of LSE_i * log2(e).  Parts
+  // go kBatch at a time with every load of the batch issued first (a part's
+  // O is loaded whatever its LSE, so no load waits for another); an empty
+  // part (LSE -inf) then has weight 0 and its O, which may hold anything, is
+  // never used.
+  constexpr int kBatch = 4;
   float m = -__builtin_inff(), s = 0.f, acc[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) acc[i] = 0.f;
-  for (int64_t i = 0; i < p.n_parts; ++i) {
-    const float l = lp[i * p.l_sp] * kLog2e;
-    if (l == -__builtin_inff()) continue;  // empty part: weight 0
-    float v[8];
-    load8<TI>(op + i * p.o_sp, v);
-    if (l > m) {
-      const float a = fast_exp2(m - l);  // 0 on the first non-empty part
-      s *= a;
+  for (int64_t i0 = 0; i0 < p.n_parts; i0 += kBatch) {
+    float l[kBatch], v[kBatch][8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) acc[j] *= a;
-      m = l;
+    for (int u = 0; u < kBatch; ++u) {
+      const int64_t i = i0 + u;
+      l[u] = -__builtin_inff();
+      if (i < p.n_parts) {  // uniform
+        l[u] = lp[i * p.l_sp] * kLog2e;
+        load8<TI>(op + i * p.o_sp, v[u]);
+      }
     }
-    const float w = fast_exp2(l - m);
-    s += w;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) acc[j] = __builtin_fmaf(w, v[j], acc[j]);
+    for (int u = 0; u < kBatch; ++u) {
+      if (l[u] == -__builtin_inff()) continue;  // empty (or absent) part: weight 0
+      if (l[u] > m) {
+        const float a = fast_exp2(m - l[u]);  // 0 on the first non-empty part
+        s *= a;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[j] *= a;
+        m = l[u];
+      }
+      const float w = fast_exp2(l[u] - m);
+      s += w;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[j] = __builtin_fmaf(w, v[u][j], acc[j]);
+    }
   }
   const float inv = s > 0.f ? 1.0f / s : 0.f;
 #pragma unroll
