@@ -36,14 +36,17 @@ def test_decode_shapes(dev, D, G, S):
     assert_close(lse, rl, atol=1e-4, what="decode lse")
 
 
+@pytest.mark.parametrize("D", [64, 128])
 @pytest.mark.parametrize("chunk", [128, 256, 512, 640])
-def test_decode_chunking_does_not_change_results(dev, chunk):
-    q, K, V = _dec_inputs(3, 2, 4, 4, 777, 128)
+def test_decode_chunking_does_not_change_results(dev, chunk, D):
+    """Every chunk length; at D = 64 the 512- and 640-token chunks run the
+    persistent loop with four groups in flight per wave."""
+    q, K, V = _dec_inputs(3, 2, 4, 4, 777, D)
     o, lse = _ops.decode(q.to(dev), K.to(dev), V.to(dev), 0.09, return_lse=True,
                          chunk_tokens=chunk)
     ro, rl = naive.decode(q, K, V, 0.09, 4)
-    assert_close(o, ro, what=f"chunk {chunk}")
-    assert_close(lse, rl, atol=1e-4, what=f"chunk {chunk} lse")
+    assert_close(o, ro, what=f"chunk {chunk} D={D}")
+    assert_close(lse, rl, atol=1e-4, what=f"chunk {chunk} D={D} lse")
 
 
 def test_decode_config2_full(dev):
