@@ -458,18 +458,26 @@ void prefill_kernel(PrefillParams p) {
       l_step[rb] = ls;
     }
   };
-  // Masks S(t): keys past a row (causal) or past S read -inf.  The test is
-  // wave-uniform; only the steps that reach the diagonal or S run the
-  // selects.
+  // Masks S(t): keys past a row (causal) or past S read -inf.  The tests are
+  // wave-uniform and made per 32-row block: only a block whose rows the
+  // step's keys reach, or whose keys reach S, runs the selects, and a causal
+  // block whose rows all precede the step's first key is set to -inf whole.
+  // (With two blocks, the first diagonal step leaves the lower block
+  // unmasked and the second masks the upper block whole.)
   auto mask_step = [&](int t, float16_t (&ss)[NRB]) {
     const int kh0 = t * 32;
     if ((CAUSAL && kh0 + 31 > r0) || kh0 + 32 > S) {
 #pragma unroll
       for (int rb = 0; rb < NRB; ++rb) {
-        const int lim = lim_base[rb] - kh0;
+        if (CAUSAL && kh0 >= r0 + 32 * rb + 32) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r)
-          if (8 * (r >> 2) + (r & 3) > lim) ss[rb][r] = AKT_P_NEG_INF;
+          for (int r = 0; r < 16; ++r) ss[rb][r] = AKT_P_NEG_INF;
+        } else if ((CAUSAL && kh0 + 31 > r0 + 32 * rb) || kh0 + 32 > S) {
+          const int lim = lim_base[rb] - kh0;
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            if (8 * (r >> 2) + (r & 3) > lim) ss[rb][r] = AKT_P_NEG_INF;
+        }
       }
     }
   };
