@@ -312,6 +312,11 @@ __attribute__((amdgpu_waves_per_eu(split_min_waves<D, GT>(), 8))) void split_ker
         w.ind_off = (int64_t)w.b * p.ind_sb + (int64_t)w.hq0 * p.ind_sh;
         n = p.sparse_nnz[(int64_t)w.b * p.nnz_sb + (int64_t)w.hq0 * p.nnz_sh];
         n = min(max(n, 0), p.l_max);
+        // A dense-cache row with no kept token attends to its first index
+        // slot, as the reference's PyTorch path does (it treats nnz == 0 as
+        // nnz == 1, sparsetoken_decode_flash_attention_redundant.py:191-194);
+        // with the harness's -1 padding that slot names the last row.
+        if constexpr (MODE == kModeSparseDense) n = max(n, min(1, p.l_max));
       }
       // Split c covers [c*per, min(n, (c+1)*per)); per is a multiple of 64 so
       // every split starts on a 16-token group and splits never share a group.
@@ -431,7 +436,11 @@ __attribute__((amdgpu_waves_per_eu(split_min_waves<D, GT>(), 8))) void split_ker
         rb = pc - lp * p.page_size;
       }
     } else if constexpr (MODE == kModeSparseDense) {
-      const int t = cx.ind_row[min(pos_k, t1 - 1)];
+      int t = cx.ind_row[min(pos_k, t1 - 1)];
+      // Indices follow torch indexing, as the reference's gather K[b, h, ind]
+      // does (sparsetoken_decode_flash_attention_redundant.py:196): -S <= t < 0
+      // names row S + t.
+      if (t < 0) t += p.S;
       kval = kval && t >= 0 && t < p.S;
       ra = t;
     } else {  // sparse paged

@@ -4,9 +4,12 @@
 (sparsetoken_decode_flash_attention_redundant.py:127-170): query head h of
 batch b attends only the kept tokens sparse_ind[b, h, :sparse_nnz[b, h]] of
 its kv head h // GQA_group_size.  sparse_ind is int32 [B, Hq, L_max] (-1
-padded), sparse_nnz int32 [B, Hq, 1].  Only the kept K/V rows are read.  A head
-with nnz == 0 yields zeros (the reference kernel yields NaN).
-``return_lse=True`` also returns the fp32 log-sum-exp [B, Hq].
+padded), sparse_nnz int32 [B, Hq, 1].  Only the kept K/V rows are read.
+Indices follow torch indexing as in the reference's PyTorch path (-S <= i < 0
+names row S + i), and a head with nnz == 0 attends to its first index slot,
+as that path does (:191-194: with -1 padding, the last token); the
+reference's Triton kernel yields NaN there.  Indices outside [-S, S) are
+skipped.  ``return_lse=True`` also returns the fp32 log-sum-exp [B, Hq].
 """
 from __future__ import annotations
 

@@ -94,9 +94,18 @@ def test_sparse_shapes_and_splits(dev, D, splits):
 
 
 def test_sparse_empty_heads_and_out_of_range_indices(dev):
-    s = syn.sparse_config(seed=5, B=1, Hq=4, Hkv=1, S=500, D=128, kept_ratio=0.05)
+    """nnz == 0 and negative indices follow the reference's PyTorch path
+    (sparsetoken_decode_flash_attention_redundant.py:193-196: nnz == 0 reads
+    the first index slot; K[b, h, ind] wraps -S <= i < 0 to S + i), so those
+    heads are compared with the oracle; indices outside [-S, S), which that
+    gather would reject, are skipped."""
+    s = syn.sparse_config(seed=5, B=1, Hq=6, Hkv=1, S=500, D=128, kept_ratio=0.05)
     ind, nnz = _sparse_lists(s)
-    nnz[0, 1, 0] = 0                                 # empty head -> zeros, lse -inf
+    nnz[0, 1, 0] = 0                                 # empty head, slot 0 a kept index
+    nnz[0, 4, 0] = 0                                 # empty head, slot 0 the -1 pad
+    ind[0, 4, 0] = -1
+    n5 = int(nnz[0, 5, 0])
+    ind[0, 5, n5 - 1] = -3                           # row S - 3
     ind2 = ind.clone()
     n2 = int(nnz[0, 2, 0])
     ind2[0, 2, n2 - 1] = 10 ** 6                     # out of range -> skipped
@@ -104,12 +113,14 @@ def test_sparse_empty_heads_and_out_of_range_indices(dev):
                                                    ind2.to(dev), nnz.to(dev), s.scale, s.group,
                                                    return_lse=True)
     o, lse = o.cpu(), lse.cpu()
-    assert torch.equal(o[0, 1], torch.zeros_like(o[0, 1])) and torch.isinf(lse[0, 1])
     nnz_ref = nnz.clone()
     nnz_ref[0, 2, 0] = n2 - 1
-    ro, _ = naive.sparsetoken_naive_decode(s.q, s.K, s.V, ind, nnz_ref, s.scale, s.group)
-    for h in (0, 2, 3):
+    ro, rl = naive.sparsetoken_naive_decode(s.q, s.K, s.V, ind, nnz_ref, s.scale, s.group)
+    for h in range(6):
         assert_close(o[0, h], ro[0, h], what=f"head {h}")
+        assert_close(lse[0, h], rl[0, h], atol=1e-4, what=f"head {h} lse")
+    # The harness-padded empty head reads the last row alone: its output is that V row.
+    assert_close(o[0, 4, 0], s.V[0, 0, -1].double(), atol=1e-3, what="nnz 0 -> V[S - 1]")
 
 
 # --------------------------------------------------------------------------- sparse paged
