@@ -37,6 +37,12 @@ COMMON_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-mllvm", "-amdgpu-atomic-optimizer-strategy=None",
 ]
+# Extra flags of single sources.  prefill_wide.hip holds the head-dim 192 and 256
+# prefill instances; LLVM's iterative ILP scheduler runs them 8-12% faster than
+# the default scheduler (it is 1-2% slower for the D = 64 instances in prefill.hip).
+SOURCE_FLAGS = {
+    "prefill_wide.hip": ["-mllvm", "-amdgpu-sched-strategy=iterative-ilp"],
+}
 
 
 def hipcc() -> str:
@@ -102,7 +108,8 @@ def build(jobs: int | None = None, verbose: bool = False) -> Path:
     for src in sources:
         obj = BUILD_DIR / (src.stem + ".o")
         objs.append(obj)
-        cmds.append([cc, *COMMON_FLAGS, "-c", str(src), "-o", str(obj)])
+        cmds.append([cc, *COMMON_FLAGS, *SOURCE_FLAGS.get(src.name, []), "-c", str(src), "-o",
+                     str(obj)])
     ext_out = torch_ext_path()
     ext_tmp = ext_out.with_name(ext_out.name + ".tmp")
     cmds.append(torch_ext_command(ext_tmp))

@@ -64,6 +64,29 @@
 
 namespace akt {
 
+// Kernel arguments (shared by both translation units of this file).
+struct PrefillParams {
+  const half_t* q;
+  const half_t* k;
+  const half_t* v;
+  half_t* o;
+  const void* varlen;
+  float* lse;  // optional [B, Hq, S] natural-log normaliser
+  int64_t lse_sb, lse_sh, lse_ss;
+  int64_t q_sb, q_sh, q_ss;
+  int64_t k_sb, k_sh, k_ss;
+  int64_t v_sb, v_sh, v_ss;
+  int64_t o_sb, o_sh, o_ss;
+  int B, Hq, Hkv, G, S;
+  int varlen_bits;
+  int n_rb;      // query row blocks (slots of one head) per sequence
+  int n_sg;      // slot groups (workgroups) per (batch, kv head)
+  int grid1d;    // 1: linear grid (a dimension past 65535); 0: grid (Hkv, B, n_sg)
+  int fast_div;  // 1: G * n_rb + kSlots < 2^22, slot / G through g_inv
+  float g_inv;   // 1 / G
+  float qk_scale;  // softmax_scale * log2(e)
+};
+
 namespace {
 
 constexpr int kPThreads = 256;
@@ -86,27 +109,7 @@ constexpr float kStepSumLimit = 32.0f * 256.0f;
 static_assert(kRescaleSlack == 8.0f, "kStepSumLimit assumes a slack of 8");
 #define AKT_P_NEG_INF (-__builtin_inff())
 
-struct PrefillParams {
-  const half_t* q;
-  const half_t* k;
-  const half_t* v;
-  half_t* o;
-  const void* varlen;
-  float* lse;  // optional [B, Hq, S] natural-log normaliser
-  int64_t lse_sb, lse_sh, lse_ss;
-  int64_t q_sb, q_sh, q_ss;
-  int64_t k_sb, k_sh, k_ss;
-  int64_t v_sb, v_sh, v_ss;
-  int64_t o_sb, o_sh, o_ss;
-  int B, Hq, Hkv, G, S;
-  int varlen_bits;
-  int n_rb;      // query row blocks (slots of one head) per sequence
-  int n_sg;      // slot groups (workgroups) per (batch, kv head)
-  int grid1d;    // 1: linear grid (a dimension past 65535); 0: grid (Hkv, B, n_sg)
-  int fast_div;  // 1: G * n_rb + kSlots < 2^22, slot / G through g_inv
-  float g_inv;   // 1 / G
-  float qk_scale;  // softmax_scale * log2(e)
-};
+
 
 typedef short short4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) short4_t lds_short4;
@@ -674,8 +677,25 @@ int launch_d(bool bf16, bool causal, bool varlen, const PrefillParams& p, dim3 g
 }
 
 }  // namespace
+
+// Head dims 192 and 256 are instantiated in a second translation unit of this
+// file (prefill_wide.hip, AKT_PREFILL_WIDE_TU), which the build compiles with
+// LLVM's iterative ILP machine scheduler: 8-12% faster at those head dims, and
+// 1-2% slower at D = 64, so D = 64 and 128 stay here with the default one.
+int prefill_launch_wide(int head_dim, bool bf16, bool causal, bool varlen, const PrefillParams& p,
+                        dim3 grid, hipStream_t st)
+#ifdef AKT_PREFILL_WIDE_TU
+{
+  return head_dim == 192 ? launch_d<192>(bf16, causal, varlen, p, grid, st)
+                         : launch_d<256>(bf16, causal, varlen, p, grid, st);
+}
+#else
+    ;
+#endif
+
 }  // namespace akt
 
+#ifndef AKT_PREFILL_WIDE_TU
 using namespace akt;
 
 namespace {
@@ -748,8 +768,7 @@ int prefill_impl(const void* q, const void* k, const void* v, void* o, float* ls
   const bool bf16 = dtype == AKT_DTYPE_BF16;
   if (head_dim == 64) return launch_d<64>(bf16, is_causal, is_var, p, grid, st);
   if (head_dim == 128) return launch_d<128>(bf16, is_causal, is_var, p, grid, st);
-  if (head_dim == 192) return launch_d<192>(bf16, is_causal, is_var, p, grid, st);
-  return launch_d<256>(bf16, is_causal, is_var, p, grid, st);
+  return prefill_launch_wide((int)head_dim, bf16, is_causal, is_var, p, grid, st);
 }
 }  // namespace
 
@@ -791,3 +810,4 @@ extern "C" int akt_prefill_fwd_ex(const void* q, const void* k, const void* v, v
                       q_stride, k_stride, v_stride, o_stride, lse ? lse_stride : nullptr,
                       softmax_scale, causal, varlen, varlen_bits, dtype, stream);
 }
+#endif  // AKT_PREFILL_WIDE_TU
