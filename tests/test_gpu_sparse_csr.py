@@ -113,3 +113,22 @@ def test_sparse_csr_every_row_empty(dev):
         o, lse = _ops.sparse_decode_csr(q, K, K, inds, ptr, 0.1, return_lse=True,
                                         num_splits=splits)
         assert torch.equal(o.cpu(), torch.zeros_like(o.cpu())) and torch.isinf(lse.cpu()).all()
+
+
+def test_sparse_csr_every_row_empty(dev):
+    """A CSR call with no kept index at all (inds has no elements) returns zeros
+    and LSE -inf on every row, on both caches."""
+    B, Hq, Hkv, S, D = 2, 4, 2, 300, 128
+    q = torch.randn(B, Hq, 1, D, device=dev).half()
+    K = torch.randn(B, Hkv, S, D, device=dev).half()
+    inds = torch.zeros(0, dtype=torch.int32, device=dev)
+    ptr = torch.zeros(B * Hq + 1, dtype=torch.int64, device=dev)
+    o, lse = csr.sparsetoken_flash_attention_decode_csr(q, K, K, inds, ptr, 0.1, Hq // Hkv,
+                                                        return_lse=True)
+    assert torch.equal(o, torch.zeros_like(o)) and bool(torch.isinf(lse).all())
+    pool = torch.randn(8, 2, Hkv, 16, D, device=dev).half()
+    indptr = torch.tensor([0, 4, 8], dtype=torch.int32, device=dev)
+    pages = torch.arange(8, dtype=torch.int32, device=dev)
+    o2, lse2 = csr.sparsetoken_flash_attention_decode_paged_csr(q, pool, indptr, pages, inds, ptr,
+                                                                return_lse=True)
+    assert torch.equal(o2, torch.zeros_like(o2)) and bool(torch.isinf(lse2).all())
