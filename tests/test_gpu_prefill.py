@@ -227,7 +227,7 @@ def test_prefill_nan_query_row_leaves_every_other_row_exact(dev):
     assert_close(out, ref, what="rows other than the NaN row", mask=keep)
 
 
-@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("D", [64, 128, 256])
 def test_prefill_long_sequence(dev, D):
     """An 8192-token causal sequence (128 key tiles per row block at the end)."""
     B, Hq, Hkv, S = 1, 2, 1, 8192
