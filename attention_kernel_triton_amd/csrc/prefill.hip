@@ -8,13 +8,14 @@
 //
 // Work decomposition.  A 256-thread workgroup serves one (batch, kv head) and
 // four "slots"; slot f = (query head f % G, row block f / G) of that kv head's
-// G query heads (64-row blocks at D = 64, 32-row blocks above).  With G a
-// multiple of 4 the four waves are four query heads at the same rows: they
-// share every staged K/V tile and have identical causal extents.  At D = 64 each wave owns 64 query rows as two 32-row MFMA
-// blocks that share every K and V fragment read from LDS; at larger head dims
-// one 32-row block (see rblocks_for).
+// G query heads (64-row blocks at D = 64 and in the long-sequence D = 128
+// instance, 32-row blocks otherwise).  With G a multiple of 4 the four waves
+// are four query heads at the same rows: they share every staged K/V tile and
+// have identical causal extents.  With 64-row blocks each wave owns its rows
+// as two 32-row MFMA blocks that share every K and V fragment read from LDS
+// (see rblocks_for).
 //
-// K/V staging.  Each tile of K and V (64 keys at D = 64, else 32) goes
+// K/V staging.  Each tile of K and V (64 keys with two row blocks, else 32) goes
 // global -> registers -> one of four LDS tile buffers: while tile j is
 // computed, tile j + 1 is already
 // published, tile j + 2 is being written and tile j + 3 is in flight from
@@ -92,15 +93,28 @@ namespace {
 constexpr int kPThreads = 256;
 constexpr int kSlots = 4;   // waves per workgroup
 constexpr int kNBuf = 4;    // LDS tile buffers
-// 32-row MFMA blocks per wave, query rows per slot and keys per staged tile:
-// two blocks and 64-key tiles at D = 64 (two waves per SIMD in 237 VGPRs);
-// from D = 128 one block and 32-key tiles.  At D = 128 that holds a wave in
-// 210 VGPRs and a workgroup's four K + V buffers in 64 KB, so two waves share
-// each SIMD (two blocks took 509 registers: one wave per SIMD, 4% slower); at
-// D = 192 and 256 the register budget allows one wave per SIMD either way.
-__host__ __device__ constexpr int rblocks_for(int D) { return D >= 128 ? 1 : 2; }
-__host__ __device__ constexpr int rows_for(int D) { return 32 * rblocks_for(D); }
-__host__ __device__ constexpr int tile_keys_for(int D) { return D >= 128 ? 32 : 64; }
+// 32-row MFMA blocks per wave, query rows per slot, keys per staged tile and
+// waves per SIMD of an instance: two blocks and 64-key tiles at D = 64 (two
+// waves per SIMD in 237 VGPRs); from D = 128 one block and 32-key tiles.  At
+// D = 128 that holds a wave in 210 VGPRs and a workgroup's four K + V buffers
+// in 64 KB, so two waves share each SIMD.  The LONG instance of D = 128 (for
+// sequences of kLongRowsD128 rows or more) takes two blocks and 64-key tiles
+// at one wave per SIMD (registers and AGPRs past 256, 128 KB of LDS): it is
+// 4-6% slower at 1024 rows and 3.5-5% faster from 4096, where each
+// workgroup's longer walk amortises its start.  At D = 192 and 256 the
+// register budget allows one wave per SIMD either way.
+__host__ __device__ constexpr bool two_blocks(int D, bool LONG) {
+  return D == 64 || (D == 128 && LONG);
+}
+__host__ __device__ constexpr int rblocks_for(int D, bool LONG) { return two_blocks(D, LONG) ? 2 : 1; }
+__host__ __device__ constexpr int rows_for(int D, bool LONG) { return 32 * rblocks_for(D, LONG); }
+__host__ __device__ constexpr int tile_keys_for(int D, bool LONG) {
+  return two_blocks(D, LONG) ? 64 : 32;
+}
+__host__ __device__ constexpr int waves_per_simd(int D, bool LONG) {
+  return (D == 64 || (D == 128 && !LONG)) ? 2 : 1;
+}
+constexpr int kLongRowsD128 = 4096;
 constexpr float kRescaleSlack = 8.0f;
 // Largest row sum of one 32-key step that lets P stay unchecked: below it
 // every probability is under 32 * 2^kRescaleSlack, far inside fp16's range;
@@ -195,14 +209,16 @@ __device__ __forceinline__ int div_small(int n, int d, float inv) {
   return q;
 }
 
-template <int D, bool CAUSAL, bool VARLEN, bool BF16>
-__global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 2 : 1, 2)))
+template <int D, bool CAUSAL, bool VARLEN, bool BF16, bool LONG>
+__global__ __launch_bounds__(kPThreads)
+__attribute__((amdgpu_waves_per_eu(waves_per_simd(D, LONG), 2)))
 void prefill_kernel(PrefillParams p) {
   typedef Elt<BF16> E;
   typedef typename E::v8 v8;
-  constexpr int NRB = rblocks_for(D);     // 32-row MFMA blocks per wave
-  constexpr int kRows = rows_for(D);      // query rows per slot
-  constexpr int kBN = tile_keys_for(D);   // keys per staged tile
+  static_assert(!LONG || D == 128, "only D = 128 has a long-sequence instance");
+  constexpr int NRB = rblocks_for(D, LONG);    // 32-row MFMA blocks per wave
+  constexpr int kRows = rows_for(D, LONG);     // query rows per slot
+  constexpr int kBN = tile_keys_for(D, LONG);  // keys per staged tile
   constexpr int SPT = kBN / 32;           // 32-key steps per tile
   constexpr int KS = D / 16;              // MFMA k-steps over the head dim
   constexpr int HALF = D / 2;             // head dims per lane half in S^T operands
@@ -655,25 +671,37 @@ void prefill_kernel(PrefillParams p) {
   }
 }
 
-template <int D, bool CAUSAL, bool VARLEN, bool BF16>
+template <int D, bool CAUSAL, bool VARLEN, bool BF16, bool LONG>
 int launch(const PrefillParams& p, dim3 grid, hipStream_t st) {
   KernelTimer timer;
-  timer.launch(prefill_kernel<D, CAUSAL, VARLEN, BF16>, grid, dim3(kPThreads), 0, st, p);
+  timer.launch(prefill_kernel<D, CAUSAL, VARLEN, BF16, LONG>, grid, dim3(kPThreads), 0, st, p);
   return check_launch("prefill_kernel");
 }
 
-template <int D, bool BF16>
+template <int D, bool BF16, bool LONG>
 int launch_dt(bool causal, bool varlen, const PrefillParams& p, dim3 grid, hipStream_t st) {
   if (causal)
-    return varlen ? launch<D, true, true, BF16>(p, grid, st) : launch<D, true, false, BF16>(p, grid, st);
-  return varlen ? launch<D, false, true, BF16>(p, grid, st) : launch<D, false, false, BF16>(p, grid, st);
+    return varlen ? launch<D, true, true, BF16, LONG>(p, grid, st)
+                  : launch<D, true, false, BF16, LONG>(p, grid, st);
+  return varlen ? launch<D, false, true, BF16, LONG>(p, grid, st)
+                : launch<D, false, false, BF16, LONG>(p, grid, st);
 }
 
-template <int D>
-int launch_d(bool bf16, bool causal, bool varlen, const PrefillParams& p, dim3 grid,
+template <int D, bool LONG>
+int launch_l(bool bf16, bool causal, bool varlen, const PrefillParams& p, dim3 grid,
              hipStream_t st) {
-  return bf16 ? launch_dt<D, true>(causal, varlen, p, grid, st)
-              : launch_dt<D, false>(causal, varlen, p, grid, st);
+  return bf16 ? launch_dt<D, true, LONG>(causal, varlen, p, grid, st)
+              : launch_dt<D, false, LONG>(causal, varlen, p, grid, st);
+}
+
+// long_rows selects the long-sequence instance (D = 128 only).
+template <int D>
+int launch_d(bool bf16, bool causal, bool varlen, bool long_rows, const PrefillParams& p,
+             dim3 grid, hipStream_t st) {
+  if constexpr (D == 128) {
+    if (long_rows) return launch_l<D, true>(bf16, causal, varlen, p, grid, st);
+  }
+  return launch_l<D, false>(bf16, causal, varlen, p, grid, st);
 }
 
 }  // namespace
@@ -686,8 +714,8 @@ int prefill_launch_wide(int head_dim, bool bf16, bool causal, bool varlen, const
                         dim3 grid, hipStream_t st)
 #ifdef AKT_PREFILL_WIDE_TU
 {
-  return head_dim == 192 ? launch_d<192>(bf16, causal, varlen, p, grid, st)
-                         : launch_d<256>(bf16, causal, varlen, p, grid, st);
+  return head_dim == 192 ? launch_d<192>(bf16, causal, varlen, false, p, grid, st)
+                         : launch_d<256>(bf16, causal, varlen, false, p, grid, st);
 }
 #else
     ;
@@ -752,7 +780,8 @@ int prefill_impl(const void* q, const void* k, const void* v, void* o, float* ls
   p.Hkv = (int)num_kv_heads;
   p.G = (int)(num_q_heads / num_kv_heads);
   p.S = (int)seq_len;
-  p.n_rb = (int)ceil_div(seq_len, rows_for((int)head_dim));
+  const bool long_rows = head_dim == 128 && seq_len >= kLongRowsD128;
+  p.n_rb = (int)ceil_div(seq_len, rows_for((int)head_dim, long_rows));
   p.n_sg = (int)ceil_div((int64_t)p.G * p.n_rb, kSlots);
   p.grid1d = (batch > 65535 || p.n_sg > 65535) ? 1 : 0;
   p.fast_div = ((int64_t)p.G * p.n_rb + kSlots < (1ll << 22)) ? 1 : 0;
@@ -766,8 +795,8 @@ int prefill_impl(const void* q, const void* k, const void* v, void* o, float* ls
   const bool is_var = varlen != nullptr;
   hipStream_t st = (hipStream_t)stream;
   const bool bf16 = dtype == AKT_DTYPE_BF16;
-  if (head_dim == 64) return launch_d<64>(bf16, is_causal, is_var, p, grid, st);
-  if (head_dim == 128) return launch_d<128>(bf16, is_causal, is_var, p, grid, st);
+  if (head_dim == 64) return launch_d<64>(bf16, is_causal, is_var, false, p, grid, st);
+  if (head_dim == 128) return launch_d<128>(bf16, is_causal, is_var, long_rows, p, grid, st);
   return prefill_launch_wide((int)head_dim, bf16, is_causal, is_var, p, grid, st);
 }
 }  // namespace

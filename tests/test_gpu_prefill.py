@@ -237,6 +237,36 @@ def test_prefill_long_sequence(dev, D):
     assert_close(out, ref, what=f"prefill S=8192 D={D}")
 
 
+@pytest.mark.parametrize("case", ["non-causal", "var-len", "bf16", "G=1"])
+def test_prefill_d128_long_sequence_instance(dev, case):
+    """From 4096 rows, D = 128 runs its long-sequence instance (two 32-row
+    blocks per wave, 64-key tiles, one wave per SIMD).  S = 4100 also leaves a
+    partial last row block and key tile."""
+    B, Hq, Hkv, S, D = 1, 4, 2, 4100, 128
+    if case == "G=1":
+        Hq = Hkv = 3
+    Q, K, V = _qkv(41 + len(case), B, Hq, Hkv, S, D)
+    scale, G = 1 / math.sqrt(D), Hq // Hkv
+    causal = case != "non-causal"
+    if case == "var-len":
+        B = 2
+        Q, K, V = _qkv(43, B, Hq, Hkv, S, D)
+        lens = torch.tensor([4100, 2345])
+        out = prevar.flash_attention_prefill(Q.to(dev), K.to(dev), V.to(dev), True, scale, G,
+                                             varlen=lens.to(dev)).cpu()
+        ref = naive.prefill_varlen(Q, K, V, True, scale, G, lens, dtype=torch.float32)
+        valid = (torch.arange(S)[None, :] < lens[:, None])[:, None, :, None].expand(Q.shape)
+        assert_close(out, ref, what="D=128 long var-len", mask=valid)
+        return
+    if case == "bf16":
+        Q, K, V = Q.bfloat16(), K.bfloat16(), V.bfloat16()
+    out, lse = pre.flash_attention_prefill(Q.to(dev), K.to(dev), V.to(dev), causal, scale, G,
+                                           return_lse=True)
+    ref, rl = naive.prefill(Q, K, V, causal, scale, G, dtype=torch.float32, return_lse=True)
+    assert_close(out, ref, atol=ATOL_BF16 if case == "bf16" else ATOL, what=f"D=128 long {case}")
+    assert_close(lse, rl, atol=1e-2 if case == "bf16" else 2e-3, what=f"D=128 long {case} lse")
+
+
 @pytest.mark.parametrize("D", [192, 256])
 @pytest.mark.parametrize("causal", [True, False])
 def test_prefill_head_dims_192_and_256(dev, causal, D):
