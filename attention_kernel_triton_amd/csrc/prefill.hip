@@ -711,14 +711,13 @@ int launch_d(bool bf16, bool causal, bool varlen, bool long_rows, const PrefillP
 // LLVM's iterative ILP machine scheduler: 8-12% faster at those head dims, and
 // 1-2% slower at D = 64, so D = 64 and 128 stay here with the default one.
 int prefill_launch_wide(int head_dim, bool bf16, bool causal, bool varlen, const PrefillParams& p,
-                        dim3 grid, hipStream_t st)
+                        dim3 grid, hipStream_t st);
 #ifdef AKT_PREFILL_WIDE_TU
-{
+int prefill_launch_wide(int head_dim, bool bf16, bool causal, bool varlen, const PrefillParams& p,
+                        dim3 grid, hipStream_t st) {
   return head_dim == 192 ? launch_d<192>(bf16, causal, varlen, false, p, grid, st)
                          : launch_d<256>(bf16, causal, varlen, false, p, grid, st);
 }
-#else
-    ;
 #endif
 
 }  // namespace akt
