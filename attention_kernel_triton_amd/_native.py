@@ -7,7 +7,6 @@ path: if the library is missing, every entry point raises.
 from __future__ import annotations
 
 import ctypes as C
-import os
 from pathlib import Path
 
 import torch
@@ -72,8 +71,15 @@ _SIGNATURES = {
 _lib = None
 
 
+# Version of include/akt_amd.h these bindings follow (AKT_ABI_VERSION).
+ABI_VERSION = 2
+# Bytes at the start of a decode workspace that must be zero before its first
+# use (AKT_WORKSPACE_ZERO_BYTES: the counter header and the arrival counters).
+WORKSPACE_ZERO_BYTES = 256 + 32768 * 4
+
+
 def library_path() -> Path:
-    return Path(os.environ.get("AKT_AMD_LIB", LIB_PATH))
+    return LIB_PATH
 
 
 def load() -> C.CDLL:
@@ -93,6 +99,10 @@ def load() -> C.CDLL:
         fn = getattr(lib, name)
         fn.restype = res
         fn.argtypes = args
+    if lib.akt_abi_version() != ABI_VERSION:
+        raise RuntimeError(
+            f"{path} has ABI version {lib.akt_abi_version()}, these bindings need "
+            f"{ABI_VERSION}: rebuild with `python -m attention_kernel_triton_amd.build`")
     _lib = lib
     return lib
 
@@ -162,10 +172,11 @@ _WS_CACHE: dict = {}
 def workspace(nbytes: int, device, stream=None) -> torch.Tensor | None:
     """Decode workspace for ``stream`` (default: the current stream of ``device``).
 
-    The C ABI requires the workspace's 256-byte counter header to be zero
-    before first use (each call leaves it zero) and a workspace to be reused
-    only by calls ordered on one stream, so one zero-initialised buffer is
-    kept per (device, stream) and grown when a call needs more.  ``stream`` is
+    The C ABI requires the workspace's first WORKSPACE_ZERO_BYTES (its
+    counters) to be zero before first use (each call leaves them zero) and a
+    workspace to be reused only by calls ordered on one stream, so one
+    zero-initialised buffer is kept per (device, stream) and grown when a call
+    needs more.  ``stream`` is
     the value ``stream_of`` returned for the same call.
     """
     if nbytes == 0:

@@ -92,4 +92,4 @@ extern "C" int akt_kernel_timer_read(double* total_ms, int64_t* launches) {
 
 extern "C" const char* akt_last_error(void) { return akt::g_error; }
 
-extern "C" int akt_abi_version(void) { return 1; }
+extern "C" int akt_abi_version(void) { return AKT_ABI_VERSION; }

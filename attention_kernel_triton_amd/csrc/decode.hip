@@ -136,33 +136,49 @@ __device__ bool locate_chunk(const SplitParams& p, int x, int& b_out, int& c_out
   return false;
 }
 
+// g(y) = log1p(y) - y for y > -1, without the cancellation of the direct
+// difference near 0.  With s = y / (2 + y), log1p(y) = 2 atanh(s) =
+// 2 (s + s^3/3 + s^5/5 + ...) and 2 s - y = -y s, so
+//   g(y) = -y s + 2 s^3 (1/3 + s^2/5 + s^4/7 + s^6/9 + s^8/11 + ...),
+// whose two parts never cancel for |y| < 0.25 (|s| < 1/7: the dropped terms
+// are below 1e-10 relative).  From |y| = 0.25 on, the direct difference
+// loses at most 3 bits.
+__device__ __forceinline__ float log1p_minus_id(float y) {
+  if (fabsf(y) < 0.25f) {
+    const float s = y / (2.0f + y);
+    const float s2 = s * s;
+    const float poly =
+        (1.0f / 3.0f) + s2 * ((1.0f / 5.0f) + s2 * ((1.0f / 7.0f) + s2 * ((1.0f / 9.0f) + s2 * (1.0f / 11.0f))));
+    return __builtin_fmaf(-y, s, 2.0f * s * s2 * poly);
+  }
+  return log1pf(y) - y;
+}
+
 // MagicPIG correction ln u for one token (eq. 11 of the reference's
 // attention_with_norm.png, as evaluated in
 // magicpig_sparsetoken_decode_flash_attention_redundant_var_len_paged_with_norm.py:110-160):
 //   p = 1 - acos(c) / pi (clamped to [0, 1]),  x = p^K,
 //   u = 1 - (1 - x)^L - L x (1 - x)^(L - 1),  clamped to >= 1e-10.
 // u is a difference of nearly equal terms when x is small or L is near 1, so
-// it is evaluated in fp32 in a form without that cancellation:
-//   u = 1 - (1 - x)^(L - 1) (1 + (L - 1) x)
-//     = -expm1((L - 1) log1p(-x) + log1p((L - 1) x))          (x >= 0.05)
-//   u = sum_{k >= 2} (k - 1) C(L, k) (-x)^k,  k <= 8            (x < 0.05)
-// (series truncation < 1e-9 relative; both forms agree with the fp64 formula).
+// it is evaluated in fp32 in a form without that cancellation.  With m = L - 1,
+//   u = 1 - (1 - x)^m (1 + m x) = -expm1(f),
+//   f = m log1p(-x) + log1p(m x) = m g(-x) + g(m x),   g(y) = log1p(y) - y
+// (the linear terms -m x and +m x cancel exactly), and for L >= 1 both parts
+// of f are <= 0, so nothing cancels for any x in [0, 1) and any L >= 1.  The
+// relative error of u stays within a few fp32 ulps.  Outside that domain
+// (x >= 1 from K < 0, or m x <= -1 from L < 0) the reference's formula is
+// evaluated as written, with its clamp of 1 - x to [0, 1].
 __device__ __forceinline__ float magicpig_log_u(float cosv, float K, float L) {
   const float pp = fminf(fmaxf(1.0f - acosf(cosv) * (float)M_1_PI, 0.0f), 1.0f);
   const float x = pp > 0.0f ? __expf(K * __logf(pp)) : 0.0f;
+  const float m = L - 1.0f;
+  const float mx = m * x;
   float u;
-  if (x >= 0.05f) {
-    u = -expm1f((L - 1.0f) * log1pf(-x) + log1pf((L - 1.0f) * x));
+  if (x < 1.0f && mx > -1.0f) {
+    u = -expm1f(__builtin_fmaf(m, log1p_minus_id(-x), log1p_minus_id(mx)));
   } else {
-    float c = 0.5f * L * (L - 1.0f);  // C(L, 2)
-    float xp = x * x;
-    u = c * xp;
-#pragma unroll
-    for (int k = 3; k <= 8; ++k) {
-      c *= (L - (float)(k - 1)) / (float)k;
-      xp *= -x;
-      u = __builtin_fmaf((float)(k - 1) * c, xp, u);
-    }
+    const float om = fminf(fmaxf(1.0f - x, 0.0f), 1.0f);
+    u = 1.0f - powf(om, L) - L * x * powf(om, m);
   }
   return __logf(fmaxf(u, 1e-10f));
 }
@@ -1176,6 +1192,8 @@ int launch_d(int D, int gt, const SplitParams& p, dim3 grid, hipStream_t st) {
 // unit a single chunk) need no counters.  Partials are addressed with 32-bit
 // byte offsets, so each array must stay below 2 GiB.
 constexpr int64_t kArriveSlots = 32768;
+static_assert(kCounterBytes + kArriveSlots * 4 == AKT_WORKSPACE_ZERO_BYTES,
+              "the public zero-prefix size matches the workspace layout");
 
 struct WsLayout {
   size_t arrive, extra_bytes, part_o, part_ml, total;

@@ -58,7 +58,10 @@
 // var-len causal mode the K/V rows at or beyond a sequence's length are never
 // staged (zeros are read in their place), so padding cannot reach valid rows
 // through P.V either.
+#include <float.h>
 #include <math.h>
+
+#include <cmath>
 
 #include "akt_common.hpp"
 #include "akt_host.hpp"
@@ -85,7 +88,8 @@ struct PrefillParams {
   int grid1d;    // 1: linear grid (a dimension past 65535); 0: grid (Hkv, B, n_sg)
   int fast_div;  // 1: G * n_rb + kSlots < 2^22, slot / G through g_inv
   float g_inv;   // 1 / G
-  float qk_scale;  // softmax_scale * log2(e)
+  float qk_scale;  // |softmax_scale| * log2(e), at least FLT_MIN
+  int neg_q;       // 1: softmax_scale < 0, computed as (-Q) K^T at |softmax_scale|
 };
 
 namespace {
@@ -365,6 +369,11 @@ void prefill_kernel(PrefillParams p) {
       // outputs are unspecified, and non-finite padding is kept out of every
       // computation.
       if (active && row < (VARLEN ? len : S)) v = ld16(Qh + (int64_t)row * p.q_ss + g * HALF + 8 * s);
+      // A negative scale is applied as (-Q) K^T times |scale| (sign bits
+      // flipped, exact in fp16 and bf16), so every step below sees a positive
+      // scale: the running max, the -inf mask and the overflow test keep
+      // their meaning.
+      if (p.neg_q) v ^= uint4_t{0x80008000u, 0x80008000u, 0x80008000u, 0x80008000u};
       qf[rb][s] = E::as8(v);
     }
   }
@@ -749,7 +758,7 @@ int prefill_impl(const void* q, const void* k, const void* v, void* o, float* ls
                 rows_aligned16(v, v_stride, 3) && rows_aligned16(o, o_stride, 3),
             "tensors must have 16-byte aligned rows");
   AKT_CHECK(!varlen || varlen_bits == 32 || varlen_bits == 64, "varlen_bits must be 32 or 64");
-  AKT_CHECK(softmax_scale > 0.f, "softmax_scale must be positive");
+  AKT_CHECK(std::isfinite(softmax_scale), "softmax_scale must be finite");
   AKT_CHECK(!lse || (lse_stride && aligned4(lse)), "lse needs strides and 4-byte alignment");
   // K / V tiles are read through 32-bit buffer offsets of up to 64 rows.
   AKT_CHECK(k_stride[2] >= 0 && k_stride[2] < (1 << 22) && v_stride[2] >= 0 &&
@@ -785,7 +794,13 @@ int prefill_impl(const void* q, const void* k, const void* v, void* o, float* ls
   p.grid1d = (batch > 65535 || p.n_sg > 65535) ? 1 : 0;
   p.fast_div = ((int64_t)p.G * p.n_rb + kSlots < (1ll << 22)) ? 1 : 0;
   p.g_inv = 1.0f / (float)p.G;
-  p.qk_scale = softmax_scale * kLog2e;
+  // Any finite scale: a negative one flips Q's sign in the kernel; a zero (or
+  // subnormal) one becomes FLT_MIN, whose product with any score below 2^100
+  // in magnitude lies within 2^-25 of 0, so every visible key gets probability
+  // exp2(0) = 1, which is softmax at scale 0, while masked keys (-inf) still
+  // get 0.
+  p.neg_q = softmax_scale < 0.f ? 1 : 0;
+  p.qk_scale = fmaxf(fabsf(softmax_scale) * kLog2e, FLT_MIN);
   const int64_t n_wg = batch * num_kv_heads * p.n_sg;
   AKT_CHECK(n_wg < (1ll << 31), "problem too large");
   const dim3 grid = p.grid1d ? dim3((unsigned)n_wg)

@@ -90,6 +90,25 @@ at::Tensor int32_on(const char* name, const at::Tensor& t, const at::Device& dev
 
 void* ptr(const at::Tensor& t) { return t.defined() ? t.data_ptr() : nullptr; }
 
+// Shape agreement of a dense Q / K / V triple, checked before devices and
+// types (so a mismatch is reported as one on any device): 4-D tensors, K and
+// V of one shape [B, Hkv, S, D] with Q's batch and head dim, and, for
+// prefill, Q's sequence length.  The kernels size every K and V read from Q's
+// and K's shapes, so a shorter V would otherwise be read past its end.
+void check_dense_shapes(const at::Tensor& Q, const at::Tensor& K, const at::Tensor& V,
+                        bool same_seq) {
+  if (Q.dim() != 4 || K.dim() != 4 || V.dim() != 4)
+    throw py::value_error("Q, K and V must be 4-D");
+  if (K.sizes() != V.sizes())
+    throw py::value_error("K and V must have one shape, got K " + c10::str(K.sizes()) + " and V " +
+                          c10::str(V.sizes()));
+  if (K.size(0) != Q.size(0) || K.size(3) != Q.size(3) || (same_seq && K.size(2) != Q.size(2)))
+    throw py::value_error("K " + c10::str(K.sizes()) + " does not match Q " +
+                          c10::str(Q.sizes()) +
+                          (same_seq ? " in batch, sequence length or head dim"
+                                    : " in batch or head dim"));
+}
+
 struct Strides {
   int64_t v[5] = {0, 0, 0, 0, 0};
 };
@@ -135,6 +154,7 @@ py::object result(const at::Tensor& o, const at::Tensor& lse, bool return_lse) {
 py::object prefill(const at::Tensor& Q_, const at::Tensor& K_, const at::Tensor& V_, bool causal,
                    double softmax_scale, const c10::optional<at::Tensor>& varlen_,
                    bool return_lse) {
+  check_dense_shapes(Q_, K_, V_, true);
   need_gpu("Q", Q_);
   const at::ScalarType dt = Q_.scalar_type();
   if (dt != at::kHalf && dt != at::kBFloat16)
@@ -143,7 +163,6 @@ py::object prefill(const at::Tensor& Q_, const at::Tensor& K_, const at::Tensor&
   const at::Device dev = Q.device();
   same_device("K", K, dev);
   same_device("V", V, dev);
-  if (Q.dim() != 4 || K.dim() != 4) throw py::value_error("Q, K and V must be 4-D");
   const int dtype = dt == at::kBFloat16 ? AKT_DTYPE_BF16 : AKT_DTYPE_F16;
   const int64_t B = Q.size(0), H = Q.size(1), S = Q.size(2), D = Q.size(3);
   const DeviceGuard guard(dev);
@@ -182,11 +201,11 @@ py::object prefill(const at::Tensor& Q_, const at::Tensor& K_, const at::Tensor&
 // --------------------------------------------------------------------------- dense decode
 py::object decode(const at::Tensor& q_, const at::Tensor& K_, const at::Tensor& V_,
                   double softmax_scale, bool return_lse, int64_t chunk_tokens) {
+  check_dense_shapes(q_, K_, V_, false);
   at::Tensor q = half_rows("q", q_), K = half_rows("K", K_), V = half_rows("V", V_);
   const at::Device dev = q.device();
   same_device("K", K, dev);
   same_device("V", V, dev);
-  if (q.dim() != 4 || K.dim() != 4) throw py::value_error("q, K and V must be 4-D");
   const int64_t B = q.size(0), Hq = q.size(1), D = q.size(3), Hkv = K.size(1), S = K.size(2);
   const DeviceGuard guard(dev);
   at::Tensor o = at::empty({B, Hq, 1, D}, q.options());
@@ -271,11 +290,11 @@ SparseMeta sparse_meta(const at::Tensor& sparse_ind, const at::Tensor& sparse_nn
 py::object sparse_decode(const at::Tensor& q_, const at::Tensor& K_, const at::Tensor& V_,
                          const at::Tensor& sparse_ind, const at::Tensor& sparse_nnz,
                          double softmax_scale, bool return_lse, int64_t num_splits) {
+  check_dense_shapes(q_, K_, V_, false);
   at::Tensor q = half_rows("q", q_), K = half_rows("K", K_), V = half_rows("V", V_);
   const at::Device dev = q.device();
   same_device("K", K, dev);
   same_device("V", V, dev);
-  if (q.dim() != 4 || K.dim() != 4) throw py::value_error("q, K and V must be 4-D");
   const int64_t B = q.size(0), Hq = q.size(1), D = q.size(3), Hkv = K.size(1), S = K.size(2);
   SparseMeta m = sparse_meta(sparse_ind, sparse_nnz, dev, B, Hq);
   const int64_t L = m.ind.size(2);

@@ -9,11 +9,14 @@
  * entry points take a caller-owned workspace of the size reported by the
  * matching *_workspace_size() function.
  *
- * Workspace contract (all decode entry points): the first 256 bytes hold
- * scheduling counters that must be zero before a workspace is first used;
- * every call leaves them zero again when it completes.  A workspace may be
- * reused by any decode entry point, but only by calls ordered on one stream
- * (calls that overlap in time must use different workspaces).
+ * Workspace contract (all decode entry points): the first
+ * min(AKT_WORKSPACE_ZERO_BYTES, workspace size) bytes hold scheduling and
+ * per-unit arrival counters and must be zero before a workspace is first
+ * used; every call leaves them zero again when it completes.  (The counters
+ * of calls with more than 32768 units past that prefix are zero-filled by the
+ * call itself.)  A workspace may be reused by any decode entry point, but
+ * only by calls ordered on one stream (calls that overlap in time must use
+ * different workspaces).
  *
  * Tensor element types: q/k/v/o and KV pools are IEEE fp16 (akt_prefill_fwd_ex
  * also takes bf16); page tables, kept-token indices and counts are int32;
@@ -61,8 +64,13 @@ extern "C" {
 /* Message describing the last failure on the calling thread ("" if none). */
 const char* akt_last_error(void);
 
-/* ABI version of this header (bumped on any signature change). */
+/* ABI version of this header (bumped on any signature or contract change). */
+#define AKT_ABI_VERSION 2
 int akt_abi_version(void);
+
+/* Bytes at the start of a decode workspace that must be zero before its first
+ * use: a 256-byte counter header and 32768 int32 arrival counters. */
+#define AKT_WORKSPACE_ZERO_BYTES (256u + 32768u * 4u)
 
 /*
  * Causal / non-causal GQA prefill, O = softmax(scale * Q K^T [+ causal]) V.
@@ -257,8 +265,12 @@ int akt_sparse_decode_paged_fwd(const void* q, const void* kv_cache,
  * Score of kept token i: q.k_i / sqrt(head_dim) - ln(u_i) with
  *   c = q.k_i / (|q| |k_i| + 1e-8) clamped to [-1+1e-7, 1-1e-7],
  *   p = clamp(1 - acos(c)/pi, 0, 1), x = p^K,
- *   u = max(1 - (1-x)^L - L x (1-x)^(L-1), 1e-10)  (evaluated in fp64),
- * with per-(batch, q head) K, L: contiguous fp32 [batch, num_q_heads].
+ *   u = max(1 - (1-x)^L - L x (1-x)^(L-1), 1e-10),
+ * with per-(batch, q head) K, L: contiguous fp32 [batch, num_q_heads].  u is
+ * evaluated in fp32 in the equal form -expm1((L-1) g(-x) + g((L-1) x)),
+ * g(y) = log1p(y) - y, which does not cancel for x in [0, 1) and L >= 1 (a
+ * few fp32 ulps of relative error in u); x >= 1 or (L-1) x <= -1 fall back to
+ * the formula as written.
  * Workspace size: akt_sparse_decode_workspace_size().
  */
 int akt_magicpig_decode_paged_fwd(const void* q, const void* kv_cache,

@@ -7,6 +7,7 @@ import re
 from pathlib import Path
 
 import pytest
+import torch
 
 from attention_kernel_triton_amd import _native as N
 
@@ -29,7 +30,7 @@ def test_library_exports_every_declared_symbol():
     lib = N.load()
     for name in declared_symbols():
         assert hasattr(lib, name), name
-    assert lib.akt_abi_version() == 1
+    assert lib.akt_abi_version() == N.ABI_VERSION == 2
 
 
 def _i64(*v):
@@ -226,3 +227,28 @@ def test_noalloc_paged_decode_rejects_workspace_past_its_array():
                                           256, 32, 8, 128, 16, 400000, 400000, qs, kvs, 0.088, 0,
                                           None)
     assert rc == 1 and b"no-allocation" in lib.akt_last_error()
+
+
+def test_host_layer_rejects_mismatched_k_and_v():
+    """K and V must have one shape that agrees with Q (batch, head dim and, for
+    prefill, sequence length) before any kernel sizes a read from them.  The
+    compiled host layer checks shapes before devices, so CPU tensors show it."""
+    from attention_kernel_triton_amd import _ops
+    Q = torch.zeros(1, 4, 8, 64, dtype=torch.float16)
+    K = torch.zeros(1, 2, 8, 64, dtype=torch.float16)
+    with pytest.raises(ValueError, match="one shape"):
+        _ops.prefill(Q, K, K[:, :, :4], True, 0.1)
+    with pytest.raises(ValueError, match="does not match Q"):
+        _ops.prefill(Q, K[:, :, :4], K[:, :, :4], True, 0.1)
+    with pytest.raises(ValueError, match="does not match Q"):
+        _ops.prefill(Q, K[..., :32], K[..., :32], True, 0.1)
+    q = torch.zeros(1, 4, 1, 64, dtype=torch.float16)
+    with pytest.raises(ValueError, match="one shape"):
+        _ops.decode(q, K, K[:, :, :4], 0.1)
+    with pytest.raises(ValueError, match="does not match Q"):
+        _ops.decode(q, torch.zeros(2, 2, 8, 64, dtype=torch.float16),
+                    torch.zeros(2, 2, 8, 64, dtype=torch.float16), 0.1)
+    ind = torch.zeros(1, 4, 8, dtype=torch.int32)
+    nnz = torch.ones(1, 4, 1, dtype=torch.int32)
+    with pytest.raises(ValueError, match="one shape"):
+        _ops.sparse_decode(q, K, K[:, :1], ind, nnz, 0.1)

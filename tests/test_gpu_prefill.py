@@ -280,3 +280,32 @@ def test_prefill_head_dims_192_and_256(dev, causal, D):
     ref, rl = naive.prefill(Q, K, V, causal, 1 / math.sqrt(D), Hq // Hkv, return_lse=True)
     assert_close(out, ref, what=f"D={D} causal={causal}")
     assert_close(lse, rl, atol=2e-3, what=f"D={D} lse causal={causal}")
+
+
+@pytest.mark.parametrize("D", [64, 128, 256])
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("scale", [-0.125, 0.0, -1.5])
+def test_prefill_any_finite_softmax_scale(dev, D, causal, scale):
+    """The reference's naive path takes any scale (prefill_flash_attention.py:415-425).
+    A negative scale runs as (-Q) K^T at |scale|; scale 0 weights every visible key
+    equally, and its LSE is ln(number of visible keys)."""
+    B, Hq, Hkv, S = 1, 4, 1, 300
+    Q, K, V = _qkv(int(100 * abs(scale)) + D + causal, B, Hq, Hkv, S, D)
+    out, lse = pre.flash_attention_prefill(Q.to(dev), K.to(dev), V.to(dev), causal, scale,
+                                           Hq // Hkv, return_lse=True)
+    ref, rl = naive.prefill(Q, K, V, causal, scale, Hq // Hkv, return_lse=True)
+    assert_close(out, ref, what=f"scale={scale} D={D} causal={causal}")
+    assert_close(lse, rl, atol=2e-3, what=f"scale={scale} lse")
+    if scale == 0.0:
+        visible = torch.arange(1, S + 1) if causal else torch.full((S,), S)
+        assert_close(lse[0, 0], torch.log(visible.double()), atol=1e-5, what="ln n at scale 0")
+
+
+def test_prefill_negative_scale_bf16(dev):
+    B, Hq, Hkv, S, D = 1, 4, 2, 200, 64
+    g = torch.Generator().manual_seed(77)
+    Q, K, V = (torch.randn(*sh, generator=g).bfloat16()
+               for sh in ((B, Hq, S, D), (B, Hkv, S, D), (B, Hkv, S, D)))
+    out = pre.flash_attention_prefill(Q.to(dev), K.to(dev), V.to(dev), True, -0.125, Hq // Hkv)
+    ref = naive.prefill(Q, K, V, True, -0.125, Hq // Hkv)
+    assert_close(out, ref, atol=ATOL_BF16, what="bf16 negative scale")

@@ -200,6 +200,69 @@ def test_magicpig_config4b_full(dev):
     assert err32 <= 2e-3
 
 
+@pytest.mark.parametrize("D,B,Hq,Hkv,min_len,max_len", [
+    (128, 1, 32, 8, 32000, 32000),  # config 4's first variant: one 32000-token sequence
+    (64, 2, 8, 2, 3000, 5000),
+])
+def test_magicpig_head_dims_64_and_128(dev, D, B, Hq, Hkv, min_len, max_len):
+    """MagicPIG at head dims 64 and 128 (the kernel instances with D/4-element K
+    slices per lane and, at D = 64, two V tokens per lane).  The D = 128 case is
+    config 4's first variant (B = 1, Hq = 32, Hkv = 8, 32000 tokens, page 16,
+    p = 0.02 kept lists from the device selection, K, L ~ U[1, 6)): O within
+    2e-3 and LSE within 1e-3 of the fp64 oracle."""
+    s = syn.sparse_paged_config(seed=40 + D, B=B, Hq=Hq, Hkv=Hkv, D=D, page=16,
+                                min_len=min_len, max_len=max_len, kept_ratio=0.02)
+    p = s.paged
+    ind, nnz = _select(s, dev)
+    o, lse = mp.magicpig_sparsetoken_flash_attention_decode_paged(
+        p.q.to(dev), p.pool.to(dev), p.indptr.to(dev), p.indices.to(dev), ind, nnz,
+        s.lsh_k.to(dev), s.lsh_l.to(dev), return_lse=True)
+    assert o.shape == (B, Hq, D)
+    r64, l64 = naive.magicpig_sparsetoken_naive_paged_attention(
+        p.q, p.pool, p.indptr, p.indices, ind.cpu(), nnz.cpu(), s.lsh_k, s.lsh_l)
+    err = assert_close(o, r64, what=f"MagicPIG D={D} vs fp64 oracle")
+    assert_close(lse, l64, atol=1e-3, what=f"MagicPIG D={D} lse vs fp64 oracle")
+    print(f"MagicPIG D={D}: max abs err {err:.3e}, kept per head "
+          f"{float(nnz.float().mean()):.0f}")
+
+
+@pytest.mark.parametrize("L", [50.0, 150.0])
+def test_magicpig_many_hash_tables(dev, L):
+    """Large L (the MagicPIG paper's L = 150 and 50) with K ~ U[4, 8), where
+    x = p^K is small but L x is not: the regime where a truncated power series
+    of u in x diverges.  O within 2e-3 and LSE within 1e-3 of the fp64 oracle;
+    the test first checks that a good share of kept tokens sit in that regime."""
+    s = syn.sparse_paged_config(seed=int(L), B=2, Hq=8, Hkv=2, D=128, page=16, min_len=2000,
+                                max_len=6000, kept_ratio=0.05)
+    p = s.paged
+    g = torch.Generator().manual_seed(int(L) + 1)
+    lsh_k = torch.rand(s.lsh_k.shape, generator=g) * 4 + 4
+    lsh_l = torch.full_like(s.lsh_l, L)
+    ind, nnz = _sparse_lists(s)
+    # Share of kept tokens with x < 0.05 and L x > 1 (cosine from fp64 q, k).
+    hits = total = 0
+    for b in range(2):
+        for h in range(8):
+            n = int(nnz[b, h, 0])
+            t = ind[b, h, :n].long()
+            pages = p.indices[int(p.indptr[b]) + t // 16].long()
+            k = p.pool[pages, 0, h // 4, t % 16].double()
+            q = p.q[b, h, 0].double()
+            c = (k @ q) / (q.norm() * k.norm(dim=-1) + 1e-8)
+            x = (1 - torch.acos(c.clamp(-1 + 1e-7, 1 - 1e-7)) / math.pi) ** float(lsh_k[b, h])
+            hits += int(((x < 0.05) & (L * x > 1)).sum())
+            total += n
+    assert hits > 0.2 * total, (hits, total)
+    o, lse = mp.magicpig_sparsetoken_flash_attention_decode_paged(
+        p.q.to(dev), p.pool.to(dev), p.indptr.to(dev), p.indices.to(dev), ind.to(dev),
+        nnz.to(dev), lsh_k.to(dev), lsh_l.to(dev), return_lse=True)
+    r64, l64 = naive.magicpig_sparsetoken_naive_paged_attention(
+        p.q, p.pool, p.indptr, p.indices, ind, nnz, lsh_k, lsh_l)
+    err = assert_close(o, r64, what=f"MagicPIG L={L} vs fp64 oracle")
+    assert_close(lse, l64, atol=1e-3, what=f"MagicPIG L={L} lse vs fp64 oracle")
+    print(f"MagicPIG L={L}: max abs err {err:.3e}, {hits}/{total} tokens with x < 0.05, L x > 1")
+
+
 def test_magicpig_empty_head_and_L1_reduction(dev):
     s = syn.sparse_paged_config(seed=31, B=1, Hq=4, Hkv=1, D=256, page=16, min_len=600,
                                 max_len=900, kept_ratio=0.05)

@@ -102,8 +102,9 @@ def test_sparse_paged_and_magicpig_csr_equal_padded(dev):
     assert_close(o3, r64, what="MagicPIG CSR vs fp64 oracle")
 
 
-def test_sparse_csr_every_row_empty(dev):
-    """A CSR call whose rows are all empty (inds has no entries): zeros and -inf."""
+def test_sparse_csr_every_row_empty_forced_splits(dev):
+    """A CSR call whose rows are all empty (inds has no entries), at one and at
+    three forced splits per row: zeros and -inf."""
     B, Hq, Hkv, S, D = 1, 4, 2, 100, 128
     q = torch.randn(B, Hq, 1, D).half().to(dev)
     K = torch.randn(B, Hkv, S, D).half().to(dev)
