@@ -64,6 +64,8 @@ _SIGNATURES = {
     "akt_kept_index_from_mask": (C.c_int, [_p, _i64, _i64, _i64, _p, _p, _i64, _p, C.c_int, _p]),
     "akt_kept_index_from_uniform": (C.c_int, [_p, C.c_float, _i64, _i64, _i64, _p, _p, _i64, _p,
                                               C.c_int, _p]),
+    "akt_diag_paged_gather": (C.c_int, [_p, _p, _i64, _i64, _i64, _i64, _i64, _i64x, _p, _p]),
+    "akt_diag_stream_read": (C.c_int, [_p, _i64, _p, _p]),
     "akt_kernel_timer_enable": (C.c_int, [C.c_int]),
     "akt_kernel_timer_read": (C.c_int, [C.POINTER(C.c_double), C.POINTER(C.c_int64)]),
 }

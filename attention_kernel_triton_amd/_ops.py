@@ -266,43 +266,8 @@ def kept_indices(l_max: int, mask=None, uniform=None, kept_ratio: float | None =
     (keep where uniform < kept_ratio).  row_len (int32 [...]) limits each row.
     Returns (sparse_ind int32 [..., l_max] padded with -1, sparse_nnz int32 [..., 1]).
     """
-    src = mask if mask is not None else uniform
-    if src is None or (mask is not None and uniform is not None):
-        raise ValueError("pass exactly one of mask= or uniform=")
-    _need_gpu("mask" if mask is not None else "uniform", src)
-    lead = tuple(src.shape[:-1])
-    n = src.shape[-1]
-    rows = 1
-    for s in lead:
-        rows *= s
-    dev = src.device
-    ind = torch.empty(lead + (int(l_max),), dtype=torch.int32, device=dev)
-    nnz = torch.empty(lead + (1,), dtype=torch.int32, device=dev)
-    rl = None
-    if row_len is not None:
-        rl = _int32("row_len", row_len, dev).contiguous()
-        if rl.numel() != rows:
-            raise ValueError("row_len must have one entry per row")
-    lib = N.load()
-    if mask is not None:
-        m = src.reshape(rows, n)
-        if m.dtype == torch.bool:
-            m = m.view(torch.uint8)
-        if m.dtype != torch.uint8:
-            raise TypeError("mask must be bool or uint8")
-        m = m.contiguous()
-        rc = lib.akt_kept_index_from_mask(N.ptr(m), rows, n, n, N.ptr(rl), N.ptr(ind), int(l_max),
-                                          N.ptr(nnz), 1 if ensure_nonempty else 0, N.stream_of(m))
-        N.check(rc, "akt_kept_index_from_mask")
-    else:
-        if kept_ratio is None:
-            raise ValueError("kept_ratio is required with uniform=")
-        u = src.reshape(rows, n)
-        if u.dtype != torch.float32:
-            raise TypeError("uniform must be float32")
-        u = u.contiguous()
-        rc = lib.akt_kept_index_from_uniform(N.ptr(u), float(kept_ratio), rows, n, n, N.ptr(rl),
-                                             N.ptr(ind), int(l_max), N.ptr(nnz),
-                                             1 if ensure_nonempty else 0, N.stream_of(u))
-        N.check(rc, "akt_kept_index_from_uniform")
-    return ind, nnz
+    # Runs in the compiled host layer (csrc/torch_ops.cpp): a few microseconds of
+    # host time, less than the kernel's, so back-to-back calls keep the GPU busy.
+    return N.torch_ext().kept_indices(int(l_max), mask=mask, uniform=uniform,
+                                      kept_ratio=None if kept_ratio is None else float(kept_ratio),
+                                      row_len=row_len, ensure_nonempty=bool(ensure_nonempty))

@@ -1,5 +1,5 @@
 // Compiled host layer of the hot entry points (prefill, dense / paged /
-// sparse / MagicPIG decode): the same checks, output allocation, stream and
+// sparse / MagicPIG decode, kept-index selection): the same checks, output allocation, stream and
 // workspace handling as the package's Python wrappers, done in C++ so a
 // drop-in call costs the host a few microseconds.  It calls the C ABI of
 // libakt_amd.so (include/akt_amd.h) and nothing else; there is no fallback.
@@ -17,6 +17,7 @@
 #include <mutex>
 #include <string>
 #include <utility>
+#include <vector>
 
 #include "../../include/akt_amd.h"
 
@@ -380,6 +381,60 @@ py::object sparse_decode_paged(const at::Tensor& q_, const at::Tensor& pool_,
   return result(o, lse, return_lse);
 }
 
+// --------------------------------------------------------------------------- kept indices
+// Sorted kept-token index lists from a keep mask or uniform draws (the checks
+// and outputs of _ops.kept_indices, in C++ so a call costs the host a few
+// microseconds and back-to-back selections keep the GPU busy).
+py::tuple kept_indices(int64_t l_max, const c10::optional<at::Tensor>& mask_,
+                       const c10::optional<at::Tensor>& uniform_,
+                       const c10::optional<double>& kept_ratio,
+                       const c10::optional<at::Tensor>& row_len_, bool ensure_nonempty) {
+  const bool has_mask = mask_.has_value() && mask_->defined();
+  const bool has_uni = uniform_.has_value() && uniform_->defined();
+  if (has_mask == has_uni) throw py::value_error("pass exactly one of mask= or uniform=");
+  if (l_max < 0) throw py::value_error("l_max must be >= 0");
+  const at::Tensor& src = has_mask ? *mask_ : *uniform_;
+  need_gpu(has_mask ? "mask" : "uniform", src);
+  if (src.dim() < 1) throw py::value_error("the keep source must have a last (token) dimension");
+  const at::Device dev = src.device();
+  std::vector<int64_t> lead(src.sizes().begin(), src.sizes().end() - 1);
+  const int64_t n = src.size(-1);
+  int64_t rows = 1;
+  for (int64_t x : lead) rows *= x;
+  at::Tensor rl;
+  if (row_len_.has_value() && row_len_->defined()) {
+    rl = int32_on("row_len", *row_len_, dev).contiguous();
+    if (rl.numel() != rows) throw py::value_error("row_len must have one entry per row");
+  }
+  const DeviceGuard guard(dev);
+  std::vector<int64_t> ishape = lead, nshape = lead;
+  ishape.push_back(l_max);
+  nshape.push_back(1);
+  at::Tensor ind = at::empty(ishape, src.options().dtype(at::kInt));
+  at::Tensor nnz = at::empty(nshape, src.options().dtype(at::kInt));
+  hipStream_t st = stream_of(src);
+  if (has_mask) {
+    at::Tensor m = src.reshape({rows, n});
+    if (m.scalar_type() == at::kBool) m = m.view(at::kByte);
+    if (m.scalar_type() != at::kByte) throw py::type_error("mask must be bool or uint8");
+    m = m.contiguous();
+    check_rc(akt_kept_index_from_mask((const uint8_t*)ptr(m), rows, n, n,
+                                      (const int32_t*)ptr(rl), (int32_t*)ptr(ind), l_max,
+                                      (int32_t*)ptr(nnz), ensure_nonempty ? 1 : 0, st),
+             "akt_kept_index_from_mask");
+  } else {
+    if (!kept_ratio.has_value()) throw py::value_error("kept_ratio is required with uniform=");
+    at::Tensor u = src.reshape({rows, n});
+    if (u.scalar_type() != at::kFloat) throw py::type_error("uniform must be float32");
+    u = u.contiguous();
+    check_rc(akt_kept_index_from_uniform((const float*)ptr(u), (float)*kept_ratio, rows, n, n,
+                                         (const int32_t*)ptr(rl), (int32_t*)ptr(ind), l_max,
+                                         (int32_t*)ptr(nnz), ensure_nonempty ? 1 : 0, st),
+             "akt_kept_index_from_uniform");
+  }
+  return py::make_tuple(ind, nnz);
+}
+
 // The cached workspaces, as (device index, stream handle, buffer) tuples.
 py::list workspaces() {
   std::lock_guard<std::mutex> lk(g_ws_mu);
@@ -409,5 +464,8 @@ PYBIND11_MODULE(_akt_torch, m) {
         py::arg("sparse_nnz"), py::arg("softmax_scale") = py::none(),
         py::arg("return_lse") = false, py::arg("num_splits") = 0, py::arg("lsh_k") = py::none(),
         py::arg("lsh_l") = py::none());
+  m.def("kept_indices", &kept_indices, py::arg("l_max"), py::arg("mask") = py::none(),
+        py::arg("uniform") = py::none(), py::arg("kept_ratio") = py::none(),
+        py::arg("row_len") = py::none(), py::arg("ensure_nonempty") = true);
   m.def("workspaces", &workspaces);
 }

@@ -159,8 +159,10 @@ def _copies(nbytes_one, floor=1):
 
 # --------------------------------------------------------------------------- CPU baseline
 def _cpu_threads():
-    """The host threads the CPU baseline uses: the OMP_NUM_THREADS share when the
-    environment sets one (the GPU boxes do), else every core."""
+    """Host threads for the CPU baseline: the job's CPU share (OMP_NUM_THREADS,
+    16 on the GPU boxes) when the environment sets one, else os.cpu_count().
+    On a GPU box os.cpu_count() reports every core of the host, most of which
+    belong to other jobs, so it is recorded but not used there."""
     env = os.environ.get("OMP_NUM_THREADS", "")
     return int(env) if env.isdigit() and int(env) > 0 else (os.cpu_count() or 1)
 
@@ -176,30 +178,34 @@ def _cpu_model():
     return "unknown CPU"
 
 
-def _cpu_baseline(fn, work, unit, sample, budget_s, args):
-    """Median wall time of fn (the oracle on a bounded sample of the leg's
-    workload, `work` units of it) over runs totalling about budget_s after one
-    warm-up; one run if a single run exceeds 30 s."""
+def _cpu_baseline(fn, work, unit, sample, args, kind="port", order="fp16, the reference's op order"):
+    """Times fn (the reference's naive path restated on a bounded sample of the
+    leg's workload, `work` units of it) on the host CPU: one warm-up run, then
+    at least 5 runs and at least 2 s, and the median (and mean) reported; a
+    single run when one takes over 30 s."""
     if args.no_cpu_baseline:
         return None
     import torch
-    torch.set_num_threads(_cpu_threads())
+    threads = _cpu_threads()
+    torch.set_num_threads(threads)
     t0 = time.perf_counter()
     fn()  # warm-up
     first = time.perf_counter() - t0
     ts = [first] if first > 30.0 else []
-    while not ts or (first <= 30.0 and (len(ts) < 3 or sum(ts) < budget_s)):
+    while first <= 30.0 and (len(ts) < 5 or sum(ts) < 2.0):
         t0 = time.perf_counter()
         fn()
         ts.append(time.perf_counter() - t0)
     ts.sort()
     t = ts[len(ts) // 2]
+    mean = sum(ts) / len(ts)
     scale = 1e9 if unit == "GB/s" else 1e12
     return {"value": work / t / scale, "unit": unit, "cores": torch.get_num_threads(),
-            "kind": "port",
-            "sample": f"{sample}; median of {len(ts)} runs ({t * 1e3:.1f} ms each, "
-                      f"{sum(ts):.1f} s in all), fp32 on {torch.get_num_threads()} threads of "
-                      f"{_cpu_model()}"}
+            "kind": kind,
+            "sample": f"{sample}; {order}; median of {len(ts)} runs ({t * 1e3:.1f} ms, mean "
+                      f"{mean * 1e3:.1f} ms){' (one run: over 30 s)' if len(ts) == 1 else ''}; "
+                      f"{torch.get_num_threads()} threads (the job's CPU share; os.cpu_count() = "
+                      f"{os.cpu_count()}) of {_cpu_model()}"}
 
 
 # --------------------------------------------------------------------------- headline legs
@@ -227,16 +233,56 @@ def bench_paged(args):
                traffic=_traffic("split_kernel_paged_decode_config3.md"))
     out["tokens"] = sum(cfg.lens)
     out["input_sets"] = len(sets)
+    out["ceilings"] = _ceilings(cfg, sets, args)
     del sets
 
     def cpu():
-        from oracle import naive
-        naive.naive_paged_attention(cfg.q, cfg.pool, cfg.indptr, cfg.indices, cfg.last_len,
-                                    dtype=torch.float32)
+        from oracle import ref_order
+        ref_order.naive_paged_attention(cfg.q, cfg.pool, cfg.indptr, cfg.indices, cfg.last_len)
 
-    _log("CPU baseline: oracle naive_paged_attention on config 3")
-    out["cpu_baseline"] = _cpu_baseline(cpu, nbytes, "GB/s", "the full config 3 batch",
-                                        10.0, args)
+    _log("CPU baseline: the reference's naive_paged_attention (fp16 op order) on config 3")
+    out["cpu_baseline"] = _cpu_baseline(cpu, nbytes, "GB/s", "the full config 3 batch", args)
+    return out
+
+
+def _ceilings(cfg, sets, args):
+    """Read-rate ceilings of the headline's bytes on this device: the diagnostic
+    kernels of csrc/diag.hip read exactly the (page, kv head) K and V blocks
+    the paged decode reads (a gather over the same page tables), and the same
+    number of bytes in order (a linear read of each pool), with no arithmetic,
+    over the same rotated input sets and with the same settling and timing."""
+    import torch
+    from attention_kernel_triton_amd import _native as N
+    lib = N.load()
+    dev = sets[0].pool.device
+    sink = torch.zeros(1, dtype=torch.int32, device=dev)
+    P, _, Hkv, page, D = cfg.pool.shape
+    total = cfg.indices.numel()
+    gather_bytes = total * Hkv * page * D * 2 * 2 + 4 * total
+    pool_bytes = cfg.pool.numel() * 2
+
+    def gather(p):
+        N.check(lib.akt_diag_paged_gather(N.ptr(p.pool), N.ptr(p.indices), total, Hkv, D, page, P,
+                                          N.strides(p.pool), N.ptr(sink), N.stream_of(p.pool)),
+                "akt_diag_paged_gather")
+
+    def stream(p):
+        N.check(lib.akt_diag_stream_read(N.ptr(p.pool), pool_bytes, N.ptr(sink),
+                                         N.stream_of(p.pool)), "akt_diag_stream_read")
+
+    _log("ceiling legs: gather of config 3's blocks, linear read of its pool")
+    out = {
+        "ceiling_gather_config3": _leg(
+            "gather ceiling", [lambda p=p: gather(p) for p in sets], gather_bytes, "GB/s",
+            "paged_gather_kernel<4>", args,
+            note=f"reads every (page, kv head) K and V block of config 3's page table "
+                 f"({total} pages x {Hkv} kv heads x 8 KB) and nothing else; {len(sets)} input "
+                 "sets rotated"),
+        "ceiling_stream_read_config3": _leg(
+            "stream ceiling", [lambda p=p: stream(p) for p in sets], pool_bytes, "GB/s",
+            "stream_read_kernel", args,
+            note=f"reads each {pool_bytes} B pool in order; {len(sets)} pools rotated"),
+    }
     return out
 
 
@@ -258,13 +304,12 @@ def bench_prefill(args):
     nb = 2
 
     def cpu():
-        from oracle import naive
-        naive.prefill(cfg.Q[:nb], cfg.K[:nb], cfg.V[:nb], True, cfg.scale, cfg.group,
-                      dtype=torch.float32)
+        from oracle import ref_order
+        ref_order.prefill(cfg.Q[:nb], cfg.K[:nb], cfg.V[:nb], True, cfg.scale, cfg.group)
 
-    _log("CPU baseline: oracle prefill on 2 of 8 batches of config 0")
+    _log("CPU baseline: the reference's prefill (fp16 op order) on 2 of 8 batches of config 0")
     out["cpu_baseline"] = _cpu_baseline(cpu, flops * nb // 8, "TFLOP/s",
-                                        "2 of the 8 batches of config 0", 10.0, args)
+                                        "2 of the 8 batches of config 0", args)
     return out
 
 
@@ -288,7 +333,6 @@ def bench_legs(args):
     from attention_kernel_triton_amd.paged_kv import append_paged_kv
     dev = torch.device("cuda:0")
     legs = {}
-    budget = 4.0
 
     # ---- config 1: var-len causal prefill (compute-bound: no rotation)
     _log("leg: var-len causal prefill, config 1")
@@ -303,14 +347,14 @@ def bench_legs(args):
     lens1 = [int(x) for x in c1.varlen.tolist()]
 
     def cpu1():
-        from oracle import naive
-        naive.prefill_varlen(c1.Q[:2], c1.K[:2], c1.V[:2], True, c1.scale, c1.group,
-                             c1.varlen[:2], dtype=torch.float32)
+        from oracle import ref_order
+        ref_order.prefill_varlen(c1.Q[:2], c1.K[:2], c1.V[:2], True, c1.scale, c1.group,
+                                 c1.varlen[:2])
 
     fl1 = 4 * 64 * 64 * sum(L * (L + 1) // 2 for L in lens1[:2])
     legs["prefill_varlen_config1"]["cpu_baseline"] = _cpu_baseline(
-        cpu1, fl1, "TFLOP/s", f"the first 2 of 8 sequences of config 1 (lengths {lens1[:2]})",
-        budget, args)
+        cpu1, fl1, "TFLOP/s", f"the first 2 of 8 sequences of config 1 (lengths {lens1[:2]}; "
+        "the reference computes all 1024 rows and zeroes the padding)", args)
 
     # ---- config 2: dense GQA decode (33.7 MB: rotated)
     _log("leg: dense GQA decode, config 2")
@@ -324,11 +368,11 @@ def bench_legs(args):
     torch.cuda.empty_cache()
 
     def cpu2():
-        from oracle import naive
-        naive.decode(c2.q, c2.K, c2.V, c2.scale, c2.group, dtype=torch.float32)
+        from oracle import ref_order
+        ref_order.decode(c2.q, c2.K, c2.V, c2.scale, c2.group)
 
     legs["decode_config2"]["cpu_baseline"] = _cpu_baseline(
-        cpu2, c2.bytes(), "GB/s", "the full config 2 batch", budget, args)
+        cpu2, c2.bytes(), "GB/s", "the full config 2 batch", args)
 
     # ---- config 4a: sparse-token decode + LSE (K/V rotated)
     _log("leg: sparse-token decode, config 4a")
@@ -350,12 +394,12 @@ def bench_legs(args):
     torch.cuda.empty_cache()
 
     def cpu4():
-        from oracle import naive
-        naive.sparsetoken_naive_decode(s4.q, s4.K, s4.V, ind4c, nnz4c, s4.scale, s4.group,
-                                       dtype=torch.float32)
+        from oracle import ref_order
+        ref_order.sparsetoken_naive_decode(s4.q, s4.K, s4.V, ind4c, nnz4c, s4.scale, s4.group)
 
     legs["sparse_config4a"]["cpu_baseline"] = _cpu_baseline(
-        cpu4, b4, "GB/s", "the full config 4a batch", budget, args)
+        cpu4, b4, "GB/s", "the full config 4a batch", args,
+        order="fp16, the reference's (b, h) loop and index gathers")
 
     # ---- config 4b: sparse paged + MagicPIG decode (kept-index sets rotated)
     _log("leg: sparse paged + MagicPIG decode, config 4b")
@@ -393,20 +437,22 @@ def bench_legs(args):
     pc = s5.paged
 
     def cpu5():
-        from oracle import naive
-        naive.sparsetoken_naive_paged_attention(pc.q, pc.pool, pc.indptr, pc.indices, ind5, nnz5,
-                                                dtype=torch.float32)
+        from oracle import ref_order
+        ref_order.sparsetoken_naive_paged_attention(pc.q, pc.pool, pc.indptr, pc.indices, ind5,
+                                                    nnz5)
 
     def cpu6():
-        from oracle import naive
-        naive.magicpig_sparsetoken_naive_paged_attention(pc.q, pc.pool, pc.indptr, pc.indices,
-                                                         ind5, nnz5, s5.lsh_k, s5.lsh_l,
-                                                         dtype=torch.float32)
+        from oracle import ref_order
+        ref_order.magicpig_sparsetoken_naive_paged_attention(pc.q, pc.pool, pc.indptr, pc.indices,
+                                                             ind5, nnz5, s5.lsh_k, s5.lsh_l)
 
+    per_token = "fp16 (MagicPIG: fp32 scores) in the reference's per-token gather loop"
     legs["sparse_paged_config4b"]["cpu_baseline"] = _cpu_baseline(
-        cpu5, b5, "GB/s", "the full config 4b batch (first kept-index set)", budget, args)
+        cpu5, b5, "GB/s", "the full config 4b batch (first kept-index set)", args,
+        order=per_token)
     legs["magicpig_config4b"]["cpu_baseline"] = _cpu_baseline(
-        cpu6, b5, "GB/s", "the full config 4b batch (first kept-index set)", budget, args)
+        cpu6, b5, "GB/s", "the full config 4b batch (first kept-index set)", args,
+        order=per_token)
 
     # ---- kept-index selection over config 4b's keep draws (sets rotated)
     _log("leg: kept-index selection, config 4b draws")
@@ -432,7 +478,8 @@ def bench_legs(args):
         kept_from_uniform(u5, s5.kept_ratio, s5.l_max, rl5)
 
     legs["kept_index_config4b"]["cpu_baseline"] = _cpu_baseline(
-        cpu7, bk, "GB/s", "all 96 rows of config 4b's draws (numpy)", budget, args)
+        cpu7, bk, "GB/s", "all 96 rows of config 4b's draws", args,
+        order="the harness's rand < p, nonzero and -1 padding, restated in numpy")
 
     # ---- LSE merge of two fp16 partial states over config 0's rows (rotated)
     _log("leg: LSE merge of partial states")
@@ -455,7 +502,8 @@ def bench_legs(args):
         naive.merge_states(mo_c, ml_c, dtype=torch.float32)
 
     legs["merge_states"]["cpu_baseline"] = _cpu_baseline(
-        cpu8, mb // 16, "GB/s", "1/16 of the rows", budget, args)
+        cpu8, mb // 16, "GB/s", "1/16 of the rows", args,
+        order="fp32 log-sum-exp merge in torch (no reference counterpart)")
 
     # ---- paged KV append: 32 sequences x 1024 tokens into random pages (rotated)
     _log("leg: paged KV append (prefill-sized)")
@@ -491,8 +539,8 @@ def bench_legs(args):
                      indptr[: nb_cpu + 1].numpy(), perm.numpy(), last[:nb_cpu].numpy())
 
     legs["paged_append"]["cpu_baseline"] = _cpu_baseline(
-        cpu9, 8 * nb_cpu * T * Hkv * D, "GB/s",
-        f"{nb_cpu} of the {Bq} sequences (numpy, one token at a time)", budget, args)
+        cpu9, 8 * nb_cpu * T * Hkv * D, "GB/s", f"{nb_cpu} of the {Bq} sequences", args,
+        order="numpy, one token at a time (no reference counterpart)")
     # HBM bytes per launch of each leg's kernel, from the committed counter summary.
     for key, leg in legs.items():
         if leg["roofline"]["traffic"] is None:
@@ -545,6 +593,7 @@ def main():
         res["config"].update({"bytes_per_step": pg.pop("work_per_step"), "tokens": pg["tokens"]})
         # Untimed steps before the W warm-up steps (GPU clocks ramp up under load).
         res["settle"] = pg.pop("settle")
+        res.setdefault("legs", {}).update(pg.pop("ceilings"))
         torch.cuda.empty_cache()
     if args.only in ("all", "headline", "prefill"):
         pf = bench_prefill(args)
@@ -556,7 +605,7 @@ def main():
                         "ms_per_step": pf["ms_per_step"], "roofline": pf["roofline"]})
         torch.cuda.empty_cache()
     if args.only in ("all", "legs"):
-        res["legs"] = bench_legs(args)
+        res.setdefault("legs", {}).update(bench_legs(args))
     if args.copy_calibration_mb:
         copy_calibration(args.copy_calibration_mb)
     print(json.dumps(res), flush=True)

@@ -373,6 +373,24 @@ int akt_kept_index_from_uniform(const float* uniform, float kept_ratio, int64_t 
 int akt_kernel_timer_enable(int enable);
 int akt_kernel_timer_read(double* total_ms, int64_t* launches);
 
+/*
+ * Read-rate ceilings (diagnostics; no counterpart in the reference, which has
+ * no bandwidth model).  They measure, on the caller's data, how fast the
+ * device streams the bytes a paged decode reads, with no arithmetic:
+ *   akt_diag_paged_gather reads the K and V block (page_size x head_dim fp16,
+ *   contiguous: kv_stride[3] == head_dim) of every (CSR page position, kv
+ *   head) pair of kv_page_indices[0 .. total_pages), as the decode kernels
+ *   address them (page ids outside [0, num_pool_pages) read page 0); blocks
+ *   of 2, 4, 8 or 16 KB.
+ *   akt_diag_stream_read reads `bytes` (a multiple of 16) from `data` in order.
+ * Both write nothing but possibly one word of `sink` (a device uint32).
+ */
+int akt_diag_paged_gather(const void* kv_cache, const int32_t* kv_page_indices,
+                          int64_t total_pages, int64_t num_kv_heads, int64_t head_dim,
+                          int64_t page_size, int64_t num_pool_pages, const int64_t kv_stride[5],
+                          uint32_t* sink, void* stream);
+int akt_diag_stream_read(const void* data, int64_t bytes, uint32_t* sink, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

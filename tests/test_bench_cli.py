@@ -17,9 +17,11 @@ def test_more_than_one_gpu_is_refused_with_a_message():
     assert "one GPU" in msg["error"]
 
 
-def test_cpu_baseline_spends_its_budget_and_takes_the_median():
+def test_cpu_baseline_runs_five_times_and_two_seconds_and_takes_the_median():
+    """The CPU-baseline timer: one warm-up run, then at least 5 runs and at least
+    2 s in all, reporting the median run."""
     import bench
-    durations = iter([0.03, 0.01, 0.02] + [0.01] * 100)
+    durations = iter([0.05, 0.3, 0.1, 0.2, 0.25, 0.15] + [0.3] * 100)
     calls = []
 
     def fn():
@@ -29,10 +31,12 @@ def test_cpu_baseline_spends_its_budget_and_takes_the_median():
     class Args:
         no_cpu_baseline = False
 
-    r = bench._cpu_baseline(fn, 1e9, "GB/s", "a sample", 0.05, Args)
+    r = bench._cpu_baseline(fn, 1e9, "GB/s", "a sample", Args)
     runs = int(r["sample"].split("median of ")[1].split()[0])
-    assert runs >= 3 and len(calls) == runs + 1  # one warm-up call
+    assert runs >= 5 and len(calls) == runs + 1  # one warm-up call
+    assert runs == 9  # 0.3 + 0.1 + 0.2 + 0.25 + 0.15 + 4 x 0.3 >= 2 s
     assert r["kind"] == "port" and r["cores"] >= 1 and r["unit"] == "GB/s"
-    assert 1 / 0.03 < r["value"] < 1 / 0.009  # 1 GB over the median run of 10-20 ms
+    assert 1 / 0.31 < r["value"] < 1 / 0.24  # 1 GB over the median run (0.25-0.3 s)
+    assert "the job's CPU share" in r["sample"] and "op order" in r["sample"]
     Args.no_cpu_baseline = True
-    assert bench._cpu_baseline(fn, 1e9, "GB/s", "a sample", 0.05, Args) is None
+    assert bench._cpu_baseline(fn, 1e9, "GB/s", "a sample", Args) is None
