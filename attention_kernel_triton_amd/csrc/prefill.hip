@@ -22,10 +22,13 @@
 // HBM, and one barrier per tile both publishes a tile and retires tile j - 2's
 // buffer.  (Direct global -> LDS copies would be waited for before every
 // transposing LDS read, which defeats the prefetch.)  Rows are stored without
-// padding; 16-byte chunk c of row r sits at chunk position c ^ swz(r), which
-// keeps both the 16-byte K reads (8 consecutive rows, one chunk) and the
-// transposing V reads (4 rows x 2 chunks per 16 lanes) free of bank
-// conflicts.  Rows past the keys a tile may use fall outside the tile's
+// padding; 16-byte chunk c of row r sits at chunk position c ^ tswz<D>(r).
+// gfx950's LDS has 64 four-byte banks; a 16-byte access serves 16 lanes per
+// cycle and an 8-byte one 32 (measured with SQ_LDS_BANK_CONFLICT on single
+// access patterns).  The swizzle keeps the 16-byte K reads (16 consecutive
+// rows, one chunk each), the transposing V reads (4 rows x 4 chunks x 2 halves
+// per 32 lanes) and the tile stores free of bank conflicts at every head dim.
+// Rows past the keys a tile may use fall outside the tile's
 // buffer-resource range and read as zeros, so every staged value is finite
 // and no read leaves the tensor.
 //
@@ -172,10 +175,22 @@ struct Elt<true> {
   }
 };
 
-// Chunk-position swizzle of a tile row (see the header comment).  Any 8
-// consecutive rows get distinct values, and rows 4i..4i+3 get values that
-// differ in bits 1..2.
-__device__ __forceinline__ int swz(int r) { return ((r & 3) << 1) | ((r >> 2) & 1); }
+// Chunk-position swizzle of a K / V tile row (see the header comment); a
+// function of r mod 16, with tswz(r + 8) = tswz(r) ^ 2.
+// - 64- and 192-dim rows (128 / 384 bytes) start on bank 0 or 32 by row
+//   parity: over 16 consecutive rows the even rows' values are a permutation
+//   of 0..7, and so are the odd rows' (K reads), and rows 4i + j and 4i + j + 2
+//   differ in bit 2 (V reads: their 4-chunk blocks land in different halves).
+// - 128- and 256-dim rows (256 / 512 bytes) all start on bank 0: 16
+//   consecutive rows get a permutation of 0..15, and rows 4i..4i+3 differ in
+//   bits 2..3.
+template <int D>
+__device__ __forceinline__ int tswz(int r) {
+  if constexpr (D == 64 || D == 192) return (((r >> 1) & 1) << 2) | ((r >> 2) & 3);
+  else return ((r & 3) << 2) | ((r >> 2) & 3);
+}
+// Chunk-position swizzle of the epilogue's O staging rows.
+__device__ __forceinline__ int eswz(int r) { return ((r & 3) << 1) | ((r >> 2) & 1); }
 
 // Workgroup -> (batch, kv head, slot group).  The linear workgroup id is
 // kvh + Hkv (b + B rank): causal work is issued heaviest slot group (lowest
@@ -297,7 +312,7 @@ void prefill_kernel(PrefillParams p) {
 
   // ---- K/V tile staging through registers: chunk i of this thread is
   // 16-byte chunk tid + 256 i of the K (then V) tile: row st_r[i], global
-  // chunk st_c[i], stored at chunk position st_c[i] ^ swz(row).  Tile j is
+  // chunk st_c[i], stored at chunk position st_c[i] ^ tswz(row).  Tile j is
   // read through a buffer resource based at its first row whose range ends
   // with row min(64, key_lim - 64 j) - 1: rows past it read as zeros, and the
   // per-lane offsets are loop invariants, so a tile costs no address VALU.
@@ -335,7 +350,7 @@ void prefill_kernel(PrefillParams p) {
     for (int i = 0; i < PER_T; ++i) {
       const int q = tid + i * kPThreads;
       const int r = q / CPR, cc = q % CPR;
-      const int off = r * ROWB + ((cc ^ swz(r)) * 16);
+      const int off = r * ROWB + ((cc ^ tswz<D>(r)) * 16);
       *reinterpret_cast<uint4_t*>(buf + off) = kd[i];
       *reinterpret_cast<uint4_t*>(buf + TILEB + off) = vd[i];
     }
@@ -346,16 +361,21 @@ void prefill_kernel(PrefillParams p) {
   // K rows for S^T: key l32 of the step, chunks g * HALF / 8 + s.
   int koff[KS];
 #pragma unroll
-  for (int s = 0; s < KS; ++s) koff[s] = l32 * ROWB + (((g * HALF / 8) + s) ^ swz(l32)) * 16;
+  for (int s = 0; s < KS; ++s) koff[s] = l32 * ROWB + (((g * HALF / 8) + s) ^ tswz<D>(l32)) * 16;
   // V^T via tr16: source lane s16 addresses key 4g + s16 / 4 of each 16-key
-  // block and dims 32n + 16 * ((lane >> 4) & 1) + 4 * (s16 % 4).
+  // block and dims 32n + 16 * ((lane >> 4) & 1) + 4 * (s16 % 4).  The second
+  // 8 keys of a 16-key block sit 8 rows on, where the swizzle differs by 2
+  // (voffh); 16 and 32 rows on it repeats.
   const int s16 = lane & 15;
   const int vrow = 4 * g + (s16 >> 2);
   const int vcl = 2 * ((lane >> 4) & 1) + ((s16 & 3) >> 1);
-  int voff[NT];
+  int voff[NT], voffh[NT];
 #pragma unroll
-  for (int n = 0; n < NT; ++n)
-    voff[n] = TILEB + vrow * ROWB + (((4 * n + vcl) ^ swz(vrow)) * 16) + (s16 & 1) * 8;
+  for (int n = 0; n < NT; ++n) {
+    voff[n] = TILEB + vrow * ROWB + (((4 * n + vcl) ^ tswz<D>(vrow)) * 16) + (s16 & 1) * 8;
+    voffh[n] =
+        TILEB + (vrow + 8) * ROWB + (((4 * n + vcl) ^ tswz<D>(vrow + 8)) * 16) + (s16 & 1) * 8;
+  }
 
   // ---- Q^T fragments of the two 32-row blocks: lane -> row, dims g*HALF + 8s + e.
   v8 qf[NRB][KS];
@@ -421,9 +441,8 @@ void prefill_kernel(PrefillParams p) {
     for (int u = 0; u < 2; ++u)
 #pragma unroll
       for (int n = 0; n < NT; ++n) {
-        const char* vp = vb + voff[n] + u * 16 * ROWB;
-        const uint2 lo = ds_read_tr16(vp);
-        const uint2 hi = ds_read_tr16(vp + 8 * ROWB);
+        const uint2 lo = ds_read_tr16(vb + voff[n] + u * 16 * ROWB);
+        const uint2 hi = ds_read_tr16(vb + voffh[n] + u * 16 * ROWB);
         vf[u][n] = E::as8(uint4_t{lo.x, lo.y, hi.x, hi.y});
       }
   };
@@ -665,7 +684,7 @@ void prefill_kernel(PrefillParams p) {
         const float16_t& a = oacc[rb][n];
         const uint2 hv = {E::pack2(a[4 * q4] * inv, a[4 * q4 + 1] * inv),
                           E::pack2(a[4 * q4 + 2] * inv, a[4 * q4 + 3] * inv)};
-        const int chunk = (4 * n + q4) ^ swz(lr);
+        const int chunk = (4 * n + q4) ^ eswz(lr);
         *reinterpret_cast<uint2*>(ost + lr * ROWB + chunk * 16 + 8 * g) = hv;
       }
   }
@@ -674,7 +693,7 @@ void prefill_kernel(PrefillParams p) {
 #pragma unroll
   for (int idx = lane_e; idx < kRows * CPR; idx += 64) {
     const int lr = idx / CPR, cc = idx % CPR;
-    const uint4_t v = *reinterpret_cast<const uint4_t*>(ost + lr * ROWB + ((cc ^ swz(lr)) * 16));
+    const uint4_t v = *reinterpret_cast<const uint4_t*>(ost + lr * ROWB + ((cc ^ eswz(lr)) * 16));
     const int row = r0 + lr;
     if (row < row_lim) *reinterpret_cast<uint4_t*>(Oh + (int64_t)row * p.o_ss + 8 * cc) = v;
   }
