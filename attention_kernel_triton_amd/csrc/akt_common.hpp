@@ -146,6 +146,17 @@ __device__ __forceinline__ uint4_t ld16(const void* p) {
 }
 __device__ __forceinline__ void st16(void* p, uint4_t v) { *reinterpret_cast<uint4_t*>(p) = v; }
 
+// 64-bit LDS word shared by the waves of a workgroup, read and written whole.
+// Relaxed workgroup-scope atomics keep the LDS address space: a volatile
+// access through a generic pointer becomes a flat access, and the wait for
+// one of those also waits for every global load the wave has in flight.
+__device__ __forceinline__ void lds_store_u64(unsigned long long* p, unsigned long long v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+__device__ __forceinline__ unsigned long long lds_load_u64(const unsigned long long* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
 // Readfirstlane for 32-bit ints: moves a wave-uniform value into an SGPR.
 __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
 

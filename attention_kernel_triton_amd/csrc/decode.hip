@@ -252,7 +252,9 @@ __attribute__((amdgpu_waves_per_eu(split_min_waves<D, GT>(), 8))) void split_ker
   __shared__ int sm_ps[TABLE ? kMaxTableB : 1];
   __shared__ int sm_wtot[kWaves];
   __shared__ int sm_next;
-  __shared__ int sm_seq;  // items whose ticket thread 0 has published in sm_next
+  // The next item's ticket (low word) and the count of items whose ticket
+  // thread 0 has published (high word), written and read as one word.
+  __shared__ unsigned long long sm_tick;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -425,32 +427,65 @@ __attribute__((amdgpu_waves_per_eu(split_min_waves<D, GT>(), 8))) void split_ker
   // unit's own q row instead, which is always mapped and finite) so that no
   // load sits behind a branch: the wait counts then only cover the buffer
   // being consumed.  Index and page lookups read clamped, in-range entries.
+  // Paged caches of whole 16-token groups: a group is the 16 rows from row
+  // `slot` of one page (uniform), so each of its addresses is a uniform base
+  // plus a per-lane byte offset that is the same for every group: this lane's
+  // K row (c16) and K slice (R), and its V token (4R + i, or for D = 64
+  // 4R + 2 (c16 / 8) + i, plus v_sb bytes per i) at dims dim0.
+  const int dim0 = (D == 64) ? 8 * (c16 & 7) : VDIM * c16;
+  const int tt0 = (D == 64) ? (4 * R + 2 * (c16 >> 3)) : 4 * R;
+  uint32_t lane_kofs = 0, lane_qofs = 0, lane_v0ofs = 0, lane_dofs = 0;
+  if constexpr (MODE == kModePaged && ALIGNED) {
+    lane_kofs = (uint32_t)(c16 * (int)p.k_sb + R * KPL) * 2u;
+    lane_qofs = (uint32_t)(R * KPL) * 2u;
+    lane_v0ofs = (uint32_t)(tt0 * (int)p.v_sb + dim0) * 2u;
+    lane_dofs = (uint32_t)dim0 * 2u;
+  }
   auto issue = [&](const IssueCtx& cx, int g, Buf& bf) {
     const int t1 = cx.t1;
     const int gpos = g << 4;
+    if constexpr (MODE == kModePaged && ALIGNED) {
+      // The usable tokens of the group are a prefix (positions below t1 of
+      // a valid page).  K rows past it lie inside the page and load as they
+      // are (their scores are masked); the V rows of unusable tokens re-read
+      // the group's first row, a usable token whenever the group has one; a
+      // group without usable tokens (or with an invalid page id) reads the
+      // unit's q row instead, which is always mapped and finite.
+      const int k = (g - cx.g_begin - wave) / kWaves;
+      const int page = __builtin_amdgcn_readlane(cx.page_pref, k);
+      const int gslot = __builtin_amdgcn_readlane(cx.slot_pref, k);
+      const bool page_ok = page >= 0 && page < p.num_pool_pages;
+      const int nvalid = page_ok ? min(max(t1 - gpos, 0), 16) : 0;
+      bf.vmask = (uint32_t)((1u << nvalid) - 1u);
+      const char* kg = reinterpret_cast<const char*>(
+          page_ok ? cx.kb + (int64_t)page * p.k_sa + (int64_t)gslot * p.k_sb : cx.kb + cx.k_dummy);
+      const uint32_t ko = page_ok ? lane_kofs : lane_qofs;
+#pragma unroll
+      for (int s = 0; s < KS; ++s) bf.k[s] = ld16(kg + ko + 16 * s);
+      const char* vg = reinterpret_cast<const char*>(
+          nvalid > 0 ? cx.vb + (int64_t)page * p.v_sa + (int64_t)gslot * p.v_sb
+                     : cx.vb + cx.v_dummy);
+      const uint32_t vstep = (uint32_t)p.v_sb * 2u;
+#pragma unroll
+      for (int i = 0; i < VTOK; ++i) {
+        const uint32_t vo = tt0 + i < nvalid ? lane_v0ofs + (uint32_t)i * vstep : lane_dofs;
+#pragma unroll
+        for (int j = 0; j < VLD; ++j) bf.v[i][j] = ld16(vg + vo + 16 * j);
+      }
+      return;
+    }
     const int pos_k = gpos + c16;
-    int ra = 0, rb = 0, gpage = 0, gslot = 0;
+    int ra = 0, rb = 0;
     bool kval = pos_k < t1;
     if constexpr (MODE == kModeDense) {
       ra = pos_k;
     } else if constexpr (MODE == kModePaged) {
-      if constexpr (ALIGNED) {
-        const int k = (g - cx.g_begin - wave) / kWaves;
-        const int page = __builtin_amdgcn_readlane(cx.page_pref, k);
-        gslot = __builtin_amdgcn_readlane(cx.slot_pref, k);
-        const bool page_ok = page >= 0 && page < p.num_pool_pages;
-        kval = kval && page_ok;
-        gpage = page_ok ? page : 0;
-        ra = gpage;
-        rb = gslot + c16;
-      } else {
-        const int pc = min(pos_k, t1 - 1);  // t1 <= len, so pc's page is in the table
-        const int lp = pc / p.page_size;
-        const int page = p.indices[cx.pstart + lp];
-        kval = kval && page >= 0 && page < p.num_pool_pages;
-        ra = page;
-        rb = pc - lp * p.page_size;
-      }
+      const int pc = min(pos_k, t1 - 1);  // t1 <= len, so pc's page is in the table
+      const int lp = pc / p.page_size;
+      const int page = p.indices[cx.pstart + lp];
+      kval = kval && page >= 0 && page < p.num_pool_pages;
+      ra = page;
+      rb = pc - lp * p.page_size;
     } else if constexpr (MODE == kModeSparseDense) {
       int t = cx.ind_row[min(pos_k, t1 - 1)];
       // Indices follow torch indexing, as the reference's gather K[b, h, ind]
@@ -481,20 +516,16 @@ __attribute__((amdgpu_waves_per_eu(split_min_waves<D, GT>(), 8))) void split_ker
     }
 #pragma unroll
     for (int i = 0; i < VTOK; ++i) {
-      const int tt = (D == 64) ? (4 * R + 2 * (c16 >> 3) + i) : (4 * R + i);
+      const int tt = tt0 + i;
       const bool vv = (vmask >> tt) & 1;
       int va, vbb;
       if constexpr (MODE == kModeDense) {
         va = gpos + tt;
         vbb = 0;
-      } else if constexpr (MODE == kModePaged && ALIGNED) {
-        va = gpage;  // the page is uniform over the group
-        vbb = gslot + tt;
       } else {
         va = __shfl(ra, tt, 64);
         vbb = __shfl(rb, tt, 64);
       }
-      const int dim0 = (D == 64) ? 8 * (c16 & 7) : VDIM * c16;
       const int64_t off = (int64_t)va * p.v_sa + (int64_t)vbb * p.v_sb;
       const half_t* vr = cx.vb + (vv ? off : cx.v_dummy) + dim0;
 #pragma unroll
@@ -868,9 +899,9 @@ __attribute__((amdgpu_waves_per_eu(split_min_waves<D, GT>(), 8))) void split_ker
   // ---- drivers ---------------------------------------------------------------
   if constexpr (PERSIST) {
     int n_items;
-    // LDS starts with whatever the CU's previous workgroup left: sm_seq
+    // LDS starts with whatever the CU's previous workgroup left: sm_tick
     // must read 0 before any wave can compare it (barriers below).
-    if (tid == 0) sm_seq = 0;
+    if (tid == 0) sm_tick = 0;
     if constexpr (TABLE) {
       // Chunk prefix over sequences (block-wide exclusive scan), once.
       int carry = 0;
@@ -912,7 +943,7 @@ __attribute__((amdgpu_waves_per_eu(split_min_waves<D, GT>(), 8))) void split_ker
         if (sm_len[bb] == 0) zero_sequence(bb);
     } else {
       n_items = p.B * ((p.S + p.chunk - 1) / p.chunk) * Y;
-      __syncthreads();  // sm_seq
+      __syncthreads();  // sm_tick
     }
     // The item whose first groups the current item's last iterations
     // prefetch.  Past the last item it is the current one with an empty
@@ -929,7 +960,7 @@ __attribute__((amdgpu_waves_per_eu(split_min_waves<D, GT>(), 8))) void split_ker
     // resets both counters to zero for the next launch.
     // - Long items (NEAR, GPW >= 6): the ticket thread 0 takes after group
     //   kAtomicK names the next item.  Thread 0 publishes it in LDS after
-    //   group kPublishK (sm_next, then the item count in sm_seq) and every
+    //   group kPublishK (with the item count, in sm_tick) and every
     //   wave sets the next item up after group kTicketK, in time for the
     //   prefetch of its first groups.  When the tickets run out a workgroup
     //   has at most the rest of its current item and one more left, so the
@@ -979,18 +1010,20 @@ __attribute__((amdgpu_waves_per_eu(split_min_waves<D, GT>(), 8))) void split_ker
           if (k == kPublishK && tid == 0) {
             // Waiting for the ticket waits for the loads issued before the
             // atomic (groups up to kAtomicK + 1, all consumed) and no others.
-            // The two volatile stores stay in program order, and LDS serves
-            // one wave's operations in order.
-            *(volatile int*)&sm_next = (int)gridDim.x + ticket_raw;
-            *(volatile int*)&sm_seq = seq;
+            lds_store_u64(&sm_tick, (uint32_t)((int)gridDim.x + ticket_raw) |
+                                        ((unsigned long long)(uint32_t)seq << 32));
           }
           if (k == kTicketK) {
             // Thread 0 wrote this item's ticket after group kPublishK; a
             // wave this far ahead of wave 0 waits for it.  The previous item's
             // reads of sm_next all precede the workgroup merge's barrier,
             // which precedes thread 0's next write.
-            while (*(volatile int*)&sm_seq != seq) __builtin_amdgcn_s_sleep(1);
-            nxt = uniform(*(volatile int*)&sm_next);
+            unsigned long long tk = lds_load_u64(&sm_tick);
+            while ((int)(tk >> 32) != seq) {
+              __builtin_amdgcn_s_sleep(1);
+              tk = lds_load_u64(&sm_tick);
+            }
+            nxt = uniform((int)(uint32_t)tk);
             nx = resolve_next(nxt, i);
             make_uniform(nx);
             setup(nx, nc, qn);
@@ -1427,6 +1460,8 @@ int paged_decode_impl(const void* q, const void* kv_cache, const int32_t* kv_pag
   AKT_CHECK(rows_aligned16(q, q_stride, 3) && rows_aligned16(kv_cache, kv_stride, 4) && aligned16(o),
             "tensors must have 16-byte aligned rows");
   AKT_CHECK(chunk_ok(chunk_tokens), "chunk_tokens must be 0 (automatic), 128, 256, 512 or 640");
+  // A group's 16 rows are addressed with 32-bit byte offsets from its first.
+  AKT_CHECK(kv_stride[3] >= 0 && kv_stride[3] < (1 << 26), "kv_cache row stride out of range");
   if (batch == 0) return AKT_OK;
   const int D = (int)head_dim;
   const int G = (int)(num_q_heads / num_kv_heads);

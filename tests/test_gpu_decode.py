@@ -147,6 +147,37 @@ def test_paged_chunk_lengths(dev, chunk):
     assert_close(lse, rl, atol=1e-4, what=f"paged chunk {chunk} lse")
 
 
+@pytest.mark.parametrize("Hq,D", [(32, 128), (32, 64), (64, 128)])
+def test_paged_persistent_640_token_chunks_at_every_boundary(dev, Hq, D):
+    """The automatic chunking of a config-3-sized launch (640-token chunks, the
+    persistent scheduler) over lengths on both sides of each chunk boundary,
+    empty and one-token sequences, padded with 8192-token ones until the launch
+    picks 640-token chunks; a second call is bit-identical."""
+    from attention_kernel_triton_amd import _native
+    lib = _native.load()
+    g = torch.Generator().manual_seed(70 + D + Hq)
+    Hkv = 8
+    lens = [0, 1, 15, 16, 17, 255, 256, 257, 639, 640, 641, 913, 914, 915, 916, 1279, 1280,
+            1281, 1828, 1829, 1919, 1920, 1921, 4096] + [8192] * 13
+    B = len(lens)
+    pages = sum(-(-L // 16) for L in lens)
+    assert lib.akt_decode_paged_workspace_size(B, Hq, Hkv, D, 16, pages, 0) == \
+        lib.akt_decode_paged_workspace_size(B, Hq, Hkv, D, 16, pages, 640)
+    indptr, indices, last, P = syn.block_table(g, lens, 16)
+    pool = torch.randn(P, 2, Hkv, 16, D, generator=g).half()
+    q = torch.randn(B, Hq, 1, D, generator=g).half()
+    o, lse = pg.flash_attention_decode_paged(q.to(dev), pool.to(dev), indptr.to(dev),
+                                             indices.to(dev), last.to(dev), return_lse=True)
+    ro, rl = naive.naive_paged_attention(q, pool, indptr, indices, last)
+    nonempty = torch.tensor(lens) > 0
+    assert_close(o, ro, what=f"640-token chunks Hq={Hq} D={D}")
+    assert_close(lse, rl, atol=1e-4, what="640-token chunks lse", mask=nonempty)
+    assert torch.isinf(lse.cpu()[~nonempty]).all()
+    again = pg.flash_attention_decode_paged(q.to(dev), pool.to(dev), indptr.to(dev),
+                                            indices.to(dev), last.to(dev))
+    assert torch.equal(again, o)
+
+
 def test_paged_config3_page_relabelling_is_bit_exact(dev):
     """Renaming physical pages (and moving their contents) must not change a single bit."""
     p = syn.paged_config(B=8, min_len=256, max_len=4096)
