@@ -73,6 +73,37 @@ __device__ __forceinline__ void swap16(float v, float& a, float& b) {
   b = __uint_as_float(r[1]);
 }
 
+// Lane h of each 16-lane row, broadcast to the whole row (DPP row_newbcast:
+// one VALU move, no LDS round trip).  h must fold to a constant.
+template <int H>
+__device__ __forceinline__ uint32_t row_bcast_c(uint32_t v) {
+  static_assert(H >= 0 && H < 16, "row lane");
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x150 + H, 0xf, 0xf, false);
+}
+__device__ __forceinline__ uint32_t row_bcast(uint32_t v, int h) {
+  switch (h) {
+    case 0: return row_bcast_c<0>(v);
+    case 1: return row_bcast_c<1>(v);
+    case 2: return row_bcast_c<2>(v);
+    case 3: return row_bcast_c<3>(v);
+    case 4: return row_bcast_c<4>(v);
+    case 5: return row_bcast_c<5>(v);
+    case 6: return row_bcast_c<6>(v);
+    case 7: return row_bcast_c<7>(v);
+    case 8: return row_bcast_c<8>(v);
+    case 9: return row_bcast_c<9>(v);
+    case 10: return row_bcast_c<10>(v);
+    case 11: return row_bcast_c<11>(v);
+    case 12: return row_bcast_c<12>(v);
+    case 13: return row_bcast_c<13>(v);
+    case 14: return row_bcast_c<14>(v);
+    default: return row_bcast_c<15>(v);
+  }
+}
+__device__ __forceinline__ float row_bcast_f(float v, int h) {
+  return __uint_as_float(row_bcast(__float_as_uint(v), h));
+}
+
 // Max / sum over the two 32-lane halves of the wave (lane l and l ^ 32).
 __device__ __forceinline__ float xor32_max(float v) {
   float a, b;
@@ -139,6 +170,18 @@ __device__ __forceinline__ half8_t as_half8(uint4_t u) { return __builtin_bit_ca
 __device__ __forceinline__ uint4_t as_uint4(half8_t h) { return __builtin_bit_cast(uint4_t, h); }
 __device__ __forceinline__ float4_t as_float4u(uint4_t u) { return __builtin_bit_cast(float4_t, u); }
 __device__ __forceinline__ uint4_t as_uint4f(float4_t f) { return __builtin_bit_cast(uint4_t, f); }
+
+typedef short short4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) short4_t lds_short4;
+
+// ds_read_b64_tr_b16: within each 16-lane group, output lane i, element j is
+// component (i % 4) of the 8-byte chunk addressed by source lane 4j + i / 4.
+// If source lane s addresses row k0 + s / 4, columns c0 + 4 (s % 4) .. +3 of a
+// row-major fp16 matrix, output lane i receives rows k0..k0+3 of column c0 + i.
+__device__ __forceinline__ uint2 ds_read_tr16(const void* lds_ptr) {
+  const short4_t r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4*)(lds_ptr));
+  return __builtin_bit_cast(uint2, r);
+}
 
 // 16-byte global load / store.
 __device__ __forceinline__ uint4_t ld16(const void* p) {

@@ -37,6 +37,7 @@
 
 #include "akt_common.hpp"
 #include "akt_host.hpp"
+#include "paged_stream.hpp"
 
 namespace akt {
 
@@ -1424,8 +1425,18 @@ static int64_t paged_grid_x(int64_t total_pages, int64_t page_size, int64_t chun
   return ceil_div(total_pages * page_size, chunk) + batch;
 }
 
+// The stream-K kernel (paged_stream.hip) serves the automatic chunk length
+// whenever it can; explicit chunk lengths keep the chunked split kernel.
+static bool use_stream(int64_t chunk_tokens, int64_t batch, int64_t page_size,
+                       int64_t total_pages, int64_t Y) {
+  return chunk_tokens == 0 && paged_stream_eligible(batch, page_size, total_pages, Y);
+}
+
 static WsLayout paged_layout(int64_t batch, int64_t Y, int gt, int64_t D, int64_t page_size,
-                             int64_t total_pages, int64_t chunk) {
+                             int64_t total_pages, int64_t chunk_tokens) {
+  if (use_stream(chunk_tokens, batch, page_size, total_pages, Y))
+    return ws_layout(batch * Y, paged_stream_wave_cap((int)D, gt) + batch * Y, gt, D);
+  const int64_t chunk = paged_chunk(chunk_tokens, total_pages, page_size, Y, batch);
   return ws_layout(batch * Y, paged_grid_x(total_pages, page_size, chunk, batch) * Y, gt, D);
 }
 
@@ -1439,8 +1450,7 @@ extern "C" size_t akt_decode_paged_workspace_size(int64_t batch, int64_t num_q_h
   const int G = (int)(num_q_heads / num_kv_heads);
   const int gt = pick_gt(G, (int)head_dim);
   const int64_t Y = num_kv_heads * ceil_div(G, gt);
-  const int64_t chunk = paged_chunk(chunk_tokens, total_pages, page_size, Y, batch);
-  return paged_layout(batch, Y, gt, head_dim, page_size, total_pages, chunk).total;
+  return paged_layout(batch, Y, gt, head_dim, page_size, total_pages, chunk_tokens).total;
 }
 
 namespace akt {
@@ -1468,11 +1478,44 @@ int paged_decode_impl(const void* q, const void* kv_cache, const int32_t* kv_pag
   const int gt = pick_gt(G, D);
   const int n_hg = (int)ceil_div(G, gt);
   const int64_t Y = num_kv_heads * n_hg;
-  const int64_t chunk = paged_chunk(chunk_tokens, total_pages, page_size, Y, batch);
-  const int64_t gx = paged_grid_x(total_pages, page_size, chunk, batch);
-  const WsLayout wl = paged_layout(batch, Y, gt, D, page_size, total_pages, chunk);
+  const WsLayout wl = paged_layout(batch, Y, gt, D, page_size, total_pages, chunk_tokens);
   rc = check_workspace(wl, workspace, workspace_bytes);
   if (rc) return rc;
+  hipStream_t st = (hipStream_t)stream;
+  if (use_stream(chunk_tokens, batch, page_size, total_pages, Y)) {
+    StreamParams sp = {};
+    sp.q = (const half_t*)q;
+    sp.kbase = (const half_t*)kv_cache;
+    sp.vbase = (const half_t*)kv_cache + kv_stride[1];
+    sp.indptr = kv_page_indptr;
+    sp.indices = kv_page_indices;
+    sp.last_len = kv_last_page_len;
+    sp.o = (half_t*)o;
+    sp.lse = lse;
+    char* c = (char*)workspace;
+    sp.arrive = (int*)(c + wl.arrive);
+    sp.part_o = (float*)(c + wl.part_o);
+    sp.part_ml = (float*)(c + wl.part_ml);
+    sp.q_sb = q_stride[0];
+    sp.q_sh = q_stride[1];
+    sp.k_sa = kv_stride[0]; sp.k_head = kv_stride[2]; sp.k_sb = (int)kv_stride[3];
+    sp.v_sa = kv_stride[0]; sp.v_head = kv_stride[2]; sp.v_sb = (int)kv_stride[3];
+    sp.B = (int)batch; sp.Hq = (int)num_q_heads; sp.G = G; sp.Y = (int)Y; sp.n_hg = n_hg;
+    sp.page_size = (int)page_size;
+    sp.gpp = (int)(page_size / 16);
+    sp.total_pages = (int)total_pages;
+    sp.TG = (int)(total_pages * sp.gpp);
+    sp.N = (int)(Y * sp.TG);
+    sp.num_pool_pages = (int)(num_pool_pages < (1ll << 31) ? num_pool_pages : (1ll << 31) - 1);
+    sp.qk_scale = softmax_scale * kLog2e;
+    SplitParams cp = {};
+    cp.arrive = sp.arrive;
+    rc = clear_extra_arrivals(cp, wl, st);
+    if (rc) return rc;
+    return paged_stream_launch(sp, D, gt, st);
+  }
+  const int64_t chunk = paged_chunk(chunk_tokens, total_pages, page_size, Y, batch);
+  const int64_t gx = paged_grid_x(total_pages, page_size, chunk, batch);
 
   SplitParams p = {};
   p.q = (const half_t*)q;
@@ -1494,7 +1537,6 @@ int paged_decode_impl(const void* q, const void* kv_cache, const int32_t* kv_pag
   p.n_hg = n_hg;
   p.chunk = (int)chunk;
   p.qk_scale = softmax_scale * kLog2e;
-  hipStream_t st = (hipStream_t)stream;
   // grid.x >= batch: the non-persistent form writes empty sequences' rows from
   // workgroups blockIdx.x < batch.
   const dim3 grid((unsigned)gx, (unsigned)Y);

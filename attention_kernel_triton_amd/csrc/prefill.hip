@@ -132,18 +132,6 @@ static_assert(kRescaleSlack == 8.0f, "kStepSumLimit assumes a slack of 8");
 
 
 
-typedef short short4_t __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) short4_t lds_short4;
-
-// ds_read_b64_tr_b16: within each 16-lane group, output lane i, element j is
-// component (i % 4) of the 8-byte chunk addressed by source lane 4j + i / 4.
-// If source lane s addresses row k0 + s / 4, columns c0 + 4 (s % 4) .. +3 of a
-// row-major fp16 matrix, output lane i receives rows k0..k0+3 of column c0 + i.
-__device__ __forceinline__ uint2 ds_read_tr16(const char* lds_ptr) {
-  const short4_t r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4*)(lds_ptr));
-  return __builtin_bit_cast(uint2, r);
-}
-
 // Operand element type of a kernel instance: fp16 (v_mfma_f32_32x32x16_f16,
 // P rounded to fp16 as the reference does) or bf16 (the bf16 MFMA, P rounded
 // to bf16, since both MFMA operands share one type).  Global loads and the

@@ -228,9 +228,11 @@ def bench_paged(args):
                                                        p.last_len)
 
     _log(f"timing paged decode ({len(sets)} input sets rotated)")
-    out = _leg("config 3", [make(p) for p in sets], nbytes, "GB/s",
-               "split_kernel<128,4,kModePaged>", args,
-               traffic=_traffic("split_kernel_paged_decode_config3.md"))
+    kernel = "split_kernel<128,4,kModePaged>" if args.chunk else "paged_stream_kernel<128,4>"
+    profile = ("split_kernel_paged_decode_config3.md" if args.chunk
+               else "paged_stream_kernel_config3.md")
+    out = _leg("config 3", [make(p) for p in sets], nbytes, "GB/s", kernel, args,
+               traffic=_traffic(profile))
     out["tokens"] = sum(cfg.lens)
     out["input_sets"] = len(sets)
     out["ceilings"] = _ceilings(cfg, sets, args)

@@ -106,17 +106,19 @@ def test_workspace_sizes_scale_with_problem():
 
 
 def test_automatic_chunk_length():
-    """The automatic split-KV chunk: 640 tokens once a launch leaves each of ~512
-    resident workgroups at least 2.75 items at that length, else the smallest of
-    128/256/512 that cuts it into at most ~256 items.  The workspace size is a
-    function of the chunk, so it shows the choice."""
+    """Automatic paged decode (chunk_tokens 0) with pages of whole 16-token
+    groups runs the stream-K kernel: its workspace holds one partial slot per
+    (wave + unit), with the waves at their 4096 maximum where no device can be
+    queried (this CPU-only process).  Explicit chunk lengths keep the chunked
+    kernel's layout, and dense decode keeps choosing its chunk (512 tokens for
+    config 2)."""
     lib = N.load()
     ws = lib.akt_decode_paged_workspace_size
-    # config 3: 7208 pages of 16 tokens, 8 kv heads -> 640-token chunks
-    assert ws(32, 32, 8, 128, 16, 7208, 0) == ws(32, 32, 8, 128, 16, 7208, 640)
-    assert ws(32, 32, 8, 128, 16, 7208, 0) != ws(32, 32, 8, 128, 16, 7208, 512)
-    # a smaller pool stays at 512
-    assert ws(32, 32, 8, 128, 16, 5000, 0) == ws(32, 32, 8, 128, 16, 5000, 512)
+    # config 3: 32 sequences x 8 kv heads = 256 units of 4 heads, D = 128
+    assert ws(32, 32, 8, 128, 16, 7208, 0) == _ws(256, 4096 + 256, 4, 128)
+    assert ws(32, 32, 8, 128, 16, 7208, 0) != ws(32, 32, 8, 128, 16, 7208, 640)
+    # pages of 8 tokens (not whole groups) keep the chunked kernel at 256 tokens
+    assert ws(32, 32, 8, 128, 8, 7208, 0) == ws(32, 32, 8, 128, 8, 7208, 256)
     # config 2 (dense, 8 x 1024 tokens, 16 kv heads) stays at 512
     dws = lib.akt_decode_workspace_size
     assert dws(8, 64, 16, 1024, 64, 0) == dws(8, 64, 16, 1024, 64, 512)
@@ -215,17 +217,22 @@ def test_paged_append_validates_arguments():
     assert rc == 0  # nothing to append
 
 
-def test_noalloc_paged_decode_rejects_workspace_past_its_array():
+@pytest.mark.parametrize("batch,hq,hkv,dim,pages,chunk", [
+    (256, 32, 8, 128, 400000, 640),  # chunked kernel: partials grow with the pages
+    (1000, 256, 64, 256, 1000, 0),   # stream-K kernel: partials grow with the units
+])
+def test_noalloc_paged_decode_rejects_workspace_past_its_array(batch, hq, hkv, dim, pages, chunk):
     """The no-allocation entry point refuses, before any GPU call, a problem whose
     split-KV workspace exceeds its fixed device array (32 MiB)."""
     lib = N.load()
-    need = lib.akt_decode_paged_workspace_size(256, 32, 8, 128, 16, 400000, 0)
+    need = lib.akt_decode_paged_workspace_size(batch, hq, hkv, dim, 16, pages, chunk)
     assert need > 32 << 20
-    qs, kvs = _i64(32 * 128, 128, 128, 1), _i64(2 * 8 * 16 * 128, 8 * 16 * 128, 16 * 128, 128, 1)
+    qs = _i64(hq * dim, dim, dim, 1)
+    kvs = _i64(2 * hkv * 16 * dim, hkv * 16 * dim, 16 * dim, dim, 1)
     rc = lib.akt_decode_paged_fwd_noalloc(C.c_void_p(16), C.c_void_p(16), C.c_void_p(16),
                                           C.c_void_p(16), C.c_void_p(16), C.c_void_p(16), None,
-                                          256, 32, 8, 128, 16, 400000, 400000, qs, kvs, 0.088, 0,
-                                          None)
+                                          batch, hq, hkv, dim, 16, pages, pages, qs, kvs, 0.088,
+                                          chunk, None)
     assert rc == 1 and b"no-allocation" in lib.akt_last_error()
 
 

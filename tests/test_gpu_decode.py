@@ -148,33 +148,30 @@ def test_paged_chunk_lengths(dev, chunk):
 
 
 @pytest.mark.parametrize("Hq,D", [(32, 128), (32, 64), (64, 128)])
-def test_paged_persistent_640_token_chunks_at_every_boundary(dev, Hq, D):
-    """The automatic chunking of a config-3-sized launch (640-token chunks, the
-    persistent scheduler) over lengths on both sides of each chunk boundary,
-    empty and one-token sequences, padded with 8192-token ones until the launch
-    picks 640-token chunks; a second call is bit-identical."""
-    from attention_kernel_triton_amd import _native
-    lib = _native.load()
+@pytest.mark.parametrize("chunk", [0, 640])
+def test_paged_lengths_at_every_boundary(dev, Hq, D, chunk):
+    """Lengths on both sides of each 16-token group and 640-token chunk
+    boundary, empty and one-token sequences, padded with 8192-token ones to a
+    config-3-sized launch: the automatic path (chunk 0, the stream-K kernel,
+    whose wave ranges then cut units at many positions) and the persistent
+    chunked kernel at 640 tokens; a second call is bit-identical."""
+    from attention_kernel_triton_amd import _ops
     g = torch.Generator().manual_seed(70 + D + Hq)
     Hkv = 8
     lens = [0, 1, 15, 16, 17, 255, 256, 257, 639, 640, 641, 913, 914, 915, 916, 1279, 1280,
             1281, 1828, 1829, 1919, 1920, 1921, 4096] + [8192] * 13
     B = len(lens)
-    pages = sum(-(-L // 16) for L in lens)
-    assert lib.akt_decode_paged_workspace_size(B, Hq, Hkv, D, 16, pages, 0) == \
-        lib.akt_decode_paged_workspace_size(B, Hq, Hkv, D, 16, pages, 640)
     indptr, indices, last, P = syn.block_table(g, lens, 16)
     pool = torch.randn(P, 2, Hkv, 16, D, generator=g).half()
     q = torch.randn(B, Hq, 1, D, generator=g).half()
-    o, lse = pg.flash_attention_decode_paged(q.to(dev), pool.to(dev), indptr.to(dev),
-                                             indices.to(dev), last.to(dev), return_lse=True)
+    args = (q.to(dev), pool.to(dev), indptr.to(dev), indices.to(dev), last.to(dev))
+    o, lse = _ops.decode_paged(*args, chunk_tokens=chunk, return_lse=True)
     ro, rl = naive.naive_paged_attention(q, pool, indptr, indices, last)
     nonempty = torch.tensor(lens) > 0
-    assert_close(o, ro, what=f"640-token chunks Hq={Hq} D={D}")
-    assert_close(lse, rl, atol=1e-4, what="640-token chunks lse", mask=nonempty)
+    assert_close(o, ro, what=f"chunk {chunk} Hq={Hq} D={D}")
+    assert_close(lse, rl, atol=1e-4, what=f"chunk {chunk} lse", mask=nonempty)
     assert torch.isinf(lse.cpu()[~nonempty]).all()
-    again = pg.flash_attention_decode_paged(q.to(dev), pool.to(dev), indptr.to(dev),
-                                            indices.to(dev), last.to(dev))
+    again = _ops.decode_paged(*args, chunk_tokens=chunk)
     assert torch.equal(again, o)
 
 

@@ -72,3 +72,36 @@ def test_paged_decode_needs_only_the_documented_zero_prefix(dev, case):
         assert torch.equal(o, ro) and torch.equal(lse, rl)
         # The counters are zero again after the call.
         assert int(ws[: N.WORKSPACE_ZERO_BYTES].count_nonzero()) == 0
+
+
+# Small launches of the automatic (stream-K) path: more waves than groups
+# (some waves empty) and fewer, units cut at many positions, paired
+# (512-thread) and unpaired (256-thread) instances.
+@pytest.mark.parametrize("lens,page,Hq,Hkv,D", [
+    ([40, 300, 1], 16, 8, 2, 128),           # 46 groups, 48 waves: two empty waves
+    ([360, 27, 4, 450, 140], 48, 8, 2, 128),  # 138 groups, 144 waves
+    ([1, 16, 17, 33], 16, 8, 1, 128),        # G = 8 (256-thread instance): 7 groups, 8 waves
+    ([700, 5, 1300], 16, 16, 4, 64),
+    ([513, 2, 90], 64, 4, 2, 256),
+    ([8192, 4000, 31, 6000], 16, 32, 8, 128),  # more groups than waves
+])
+def test_paged_auto_path_on_dirty_workspace_matches_oracle(dev, lens, page, Hq, Hkv, D):
+    """Every unit's run of waves stores and counts its partials: the results
+    match the oracle on a workspace whose partial area holds garbage, and the
+    arrival counters are zero again after each of two calls."""
+    from oracle import naive
+
+    g = torch.Generator().manual_seed(sum(lens) + page + D)
+    indptr, indices, last, P = syn.block_table(g, lens, page, 3)
+    pool = torch.randn(P, 2, Hkv, page, D, generator=g).half()
+    q = torch.randn(len(lens), Hq, 1, D, generator=g).half()
+    ro, rl = naive.naive_paged_attention(q, pool, indptr, indices, last)
+    p = syn.Paged(q.to(dev), pool.to(dev), indptr.to(dev), indices.to(dev), last.to(dev), lens)
+    ws = _dirty_workspace(_need(p), dev)
+    for _ in range(2):
+        o, lse = _paged_capi(p, ws)
+        torch.cuda.synchronize(dev)
+        err = float((o.cpu().double() - ro).abs().max())
+        lerr = float((lse.cpu().double() - rl).abs().max())
+        assert err <= 2e-3 and lerr <= 1e-4, (err, lerr)
+        assert int(ws[: N.WORKSPACE_ZERO_BYTES].count_nonzero()) == 0
