@@ -49,9 +49,12 @@ __device__ __forceinline__ int last_le(const int* s, int n, int x) {
   return lo - 1;
 }
 
+// Waves per SIMD the instance is built for: two up to D = 128 (at most ~180
+// VGPRs whatever the head count: P.V accumulates in D/4 registers), one at
+// D = 256.
 template <int D, int GT>
 constexpr int stream_min_waves() {
-  return (D <= 128 && GT <= 4) ? 2 : 1;
+  return D <= 128 ? 2 : 1;
 }
 // Threads per workgroup: with two waves per SIMD, one 512-thread workgroup per
 // CU, so that the two waves sharing a SIMD (waves w and w + 4) are in one
@@ -85,9 +88,8 @@ __attribute__((amdgpu_waves_per_eu(stream_min_waves<D, GT>(), 8))) void paged_st
 
   // Sequence page ranges: sequence b owns positions [sm_s[b], sm_s[b + 1]) of
   // kv_page_indices (indptr clamped to [0, total_pages] and made
-  // non-decreasing), and its last page holds sm_ll[b] tokens.
+  // non-decreasing).
   __shared__ int sm_s[kStreamMaxBatch + 1];
-  __shared__ int sm_ll[kStreamMaxBatch];
   __shared__ int sm_wmax[kSWaves];
   // Groups each wave has consumed (paired waves only).
   __shared__ int sm_prog[kSWaves];
@@ -120,22 +122,59 @@ __attribute__((amdgpu_waves_per_eu(stream_min_waves<D, GT>(), 8))) void paged_st
     pp = pos / p.gpp;
     slice = pos - pp * p.gpp;
   };
-  // Page ids are read PD groups ahead with one vector load per group (a
-  // uniform address), the same load every iteration.  (A scalar load would be
-  // counted with the LDS accesses and, since scalar loads complete out of
-  // order, every LDS wait would then wait for it.)  la_pp / la_slice: page
-  // position and 16-row slice of the next group whose page id is fetched,
-  // advanced one group per fetch (wrapping inside the page table).
-  const auto idx_rsrc = __builtin_amdgcn_make_buffer_rsrc((void*)p.indices, 0, 0x7fffffff,
-                                                          kBufferWord3);
-  int la_pp = 0, la_slice = 0;
-  auto fetch_page = [&]() __attribute__((always_inline)) -> int {
-    const int v = __builtin_amdgcn_raw_buffer_load_b32(idx_rsrc, (uint32_t)la_pp * 4u, 0, 0);
-    if (++la_slice == p.gpp) {
-      la_slice = 0;
-      if (++la_pp == p.total_pages) la_pp = 0;
+  // ---- lookahead ------------------------------------------------------------
+  // The group PD ahead of the one being issued is "fetched": its page id and
+  // its sequence's last-page length are read with one vector load each (a
+  // uniform address), the same two loads for every group.  (A scalar load
+  // would be counted with the LDS accesses and, since scalar loads complete
+  // out of order, every LDS wait would then wait for it.)  Its position is
+  // tracked in scalar registers, advanced one group per fetch: head group
+  // la_y, page position la_pp, 16-row slice la_slice, and sequence la_b
+  // (-1 before sequence 0's pages, B past the last) with la_end, the first
+  // position past la_b's pages (la_b and la_end need the sequence table).
+  // (Sized to the tensors: a read past them returns 0 and touches no memory.)
+  const auto idx_rsrc = __builtin_amdgcn_make_buffer_rsrc((void*)p.indices, 0,
+                                                          p.total_pages * 4, kBufferWord3);
+  const auto ll_rsrc = __builtin_amdgcn_make_buffer_rsrc((void*)p.last_len, 0, p.B * 4,
+                                                         kBufferWord3);
+  int la_y = 0, la_pp = 0, la_slice = 0, la_b = -1, la_end = 0;
+  auto seq_end = [&](int b) __attribute__((always_inline)) -> int {
+    return b < p.B ? uniform(sm_s[b + 1]) : INT32_MAX;
+  };
+  // One group forward; `track`: keep la_b / la_end (the table exists).
+  auto advance = [&](bool track) __attribute__((always_inline)) {
+    if (++la_slice < p.gpp) return;
+    la_slice = 0;
+    if (++la_pp == p.total_pages) {
+      la_pp = 0;
+      ++la_y;
+      la_b = -1;
+      if (track) la_end = uniform(sm_s[0]);
     }
-    return v;
+    if (track)
+      while (la_b < p.B && la_pp >= la_end) la_end = seq_end(++la_b);
+  };
+  // Sequence of position pp from the table (the last b with start <= pp).
+  auto seek = [&](int pp) __attribute__((always_inline)) {
+    la_b = uniform(last_le(sm_s, p.B, pp));
+    la_end = la_b < 0 ? uniform(sm_s[0]) : seq_end(la_b);
+  };
+  // A fetched group: page id and last-page length (vector registers, loaded),
+  // and its position (wave-uniform).
+  struct Fetch {
+    int page, ll;
+    int b, y, slot, last;
+  };
+  auto fetch = [&](Fetch& f) __attribute__((always_inline)) {
+    f.page = __builtin_amdgcn_raw_buffer_load_b32(idx_rsrc, (uint32_t)la_pp * 4u, 0, 0);
+    const bool seq_ok = la_b >= 0 && la_b < p.B;
+    const int lb = min(max(la_b, 0), p.B - 1);
+    f.ll = __builtin_amdgcn_raw_buffer_load_b32(ll_rsrc, (uint32_t)lb * 4u, 0, 0);
+    f.b = seq_ok ? la_b : -1;
+    f.y = la_y;
+    f.slot = la_slice * 16;
+    f.last = seq_ok && la_pp == la_end - 1;
+    advance(true);
   };
 
   // ---- per-lane load offsets ------------------------------------------------
@@ -152,98 +191,66 @@ __attribute__((amdgpu_waves_per_eu(stream_min_waves<D, GT>(), 8))) void paged_st
   const uint32_t lane_dofs = (uint32_t)dim0 * 2u;
   const uint32_t vstep = (uint32_t)p.v_sb * 2u;
 
-  // ---- window metadata: lane l describes group g0 + 64 cw + l ---------------
-  // Address part (the kernel arguments only): m_ya = head group << 20 | first
-  // row of the slice.  Sequence part (the table in LDS): m_b = sequence (-1:
-  // the position belongs to none), m_nv = tokens of the slice below the
-  // sequence's length.
-  int cw = 0;
-  int m_ya = 0, m_b = -1, m_nv = 0;
-  auto describe_addr = [&](int w) __attribute__((always_inline)) {
-    const int j = min(64 * w + lane, n - 1);
-    int y, pp, slice;
-    locate(g0 + j, y, pp, slice);
-    m_ya = (y << 20) | (slice * 16);
-  };
-  auto describe_seq = [&](int w) __attribute__((always_inline)) {
-    const int j = min(64 * w + lane, n - 1);
-    int y, pp, slice;
-    locate(g0 + j, y, pp, slice);
-    const int b = last_le(sm_s, p.B, pp);
-    const bool seq_ok = b >= 0 && b < p.B;
-    int nv = 0;
-    if (seq_ok) nv = (pp == sm_s[b + 1] - 1) ? min(max(sm_ll[b] - 16 * slice, 0), 16) : 16;
-    m_b = seq_ok ? b : -1;
-    m_nv = nv;
-  };
-
   struct Buf {
     uint4_t k[KS];
     uint4_t v[VTOK][VLD];
     half8_t q[KS];  // the query fragment of the group's unit
-    int b, y, nv;   // wave-uniform: sequence (-1: none), head group, usable tokens
+    int ll;         // the sequence's last-page length (loaded)
+    // wave-uniform: sequence (-1: none or a dummy), head group, first row of
+    // the slice, whether the page is the sequence's last, valid page id
+    int b, y, slot, last, use;
+  };
+  // Usable tokens of a buffer's group: 16, or on the sequence's last page the
+  // rows below its length (clamped to [0, page_size]), 0 for invalid pages.
+  auto usable = [&](const Buf& bf) __attribute__((always_inline)) -> int {
+    if (!bf.use || bf.b < 0) return 0;
+    if (!bf.last) return 16;
+    const int ll = min(max(uniform(bf.ll), 0), p.page_size);
+    return min(max(ll - bf.slot, 0), 16);
   };
 
   // Query fragment of unit (b, y) (MFMA B operand): head hq0 + c16, dims
-  // 32s + 8R + e (the K loads' assignment); heads past the unit's read as
-  // zeros.  b < 0 (no unit) reads sequence 0's rows, so that every group
-  // issues the same loads.
+  // 32s + 8R + e (the K loads' assignment).  Columns past the unit's heads
+  // repeat head hq0: each column's scores, softmax and P.V stay in that
+  // column's lanes, and those lanes store nothing.  (Zeroing them would make
+  // the compiler wait for the loads right where they are issued.)  b < 0 (no
+  // unit) reads sequence 0's rows, so that every group issues the same loads.
   auto load_q = [&](int b, int y, half8_t (&qd)[KS]) __attribute__((always_inline)) {
     b = max(b, 0);
     const int kvh = p.n_hg == 1 ? y : y / p.n_hg;
     const int hg = y - kvh * p.n_hg;
     const int hq0 = kvh * p.G + hg * GT;
     const int nh = min(GT, p.G - hg * GT);
-    const bool hv = c16 < nh;
     const half_t* qrow =
-        p.q + (int64_t)b * p.q_sb + (int64_t)(hq0 + (hv ? c16 : 0)) * p.q_sh + 8 * R;
+        p.q + (int64_t)b * p.q_sb + (int64_t)(hq0 + (c16 < nh ? c16 : 0)) * p.q_sh + 8 * R;
 #pragma unroll
-    for (int s = 0; s < KS; ++s) {
-      uint4_t v = ld16(qrow + 32 * s);
-      if (!hv) v = uint4_t{0, 0, 0, 0};
-      qd[s] = as_half8(v);
-    }
+    for (int s = 0; s < KS; ++s) qd[s] = as_half8(ld16(qrow + 32 * s));
   };
 
-  // Sequence part of group j (j < n), into a buffer.
-  auto set_seq = [&](int j, Buf& bf) __attribute__((always_inline)) {
-    const int lw = j & 63;
-    bf.b = __builtin_amdgcn_readlane(m_b, lw);
-    bf.nv = __builtin_amdgcn_readlane(m_nv, lw);
-  };
-  // Issues group j of this wave (j >= n: a dummy group that reads the q row).
-  // Rows of a valid page are loaded whole; tokens past the usable prefix are
-  // masked when consumed.  With `seq`, the group's sequence part is filled in
-  // and its unit's q fragment is loaded with it.  Every call issues the same
-  // loads whatever the data: a load issued only on some paths would leave
-  // the compiler unsure how many loads follow a buffer's, and it would then
-  // wait for all of them before consuming it.
-  // pg[i] holds the page id of the next group issued into buffer i (groups
-  // i, i + PD, ...): taken here, and the one PD groups later fetched.
-  int pg[PD];
-  auto issue = [&](int j, Buf& bf, bool seq, int& pgi) __attribute__((always_inline)) {
-    int ya = 0;
-    const int page = uniform(pgi);
-    pgi = fetch_page();
-    bf.b = -1;
-    bf.nv = 0;
-    if (j < n) {
-      if ((j >> 6) != cw) {  // next window (LDS and VALU work only)
-        ++cw;
-        describe_addr(cw);
-        describe_seq(cw);
-      }
-      const int lw = j & 63;
-      ya = __builtin_amdgcn_readlane(m_ya, lw);
-      if (seq) set_seq(j, bf);
-    }
-    const int y = ya >> 20;
-    const int slot = ya & 0xfffff;
+  // Issues group j of this wave from its fetch record f (j >= n: a dummy
+  // group that reads the q row), then fetches group j + PD into f.
+  // `take_ll`: f's last-page length goes to the buffer (the prologue loads
+  // it into the buffer itself).  Rows of a
+  // valid page are loaded whole; tokens past the usable prefix are masked when
+  // consumed.  `seq`: the sequence is known (the table exists), so the unit's
+  // q fragment is loaded with the group.  Every call issues the same loads
+  // whatever the data: a load issued only on some paths would leave the
+  // compiler unsure how many loads follow a buffer's, and it would then wait
+  // for all of them before consuming it.
+  Fetch fr[PD];
+  auto issue = [&](int j, Buf& bf, bool seq, Fetch& f, bool take_ll)
+                   __attribute__((always_inline)) {
+    const int page = uniform(f.page);
+    const int y = f.y, slot = f.slot;
+    if (take_ll) bf.ll = f.ll;
+    bf.b = j < n ? f.b : -1;
     bf.y = y;
+    bf.slot = slot;
+    bf.last = f.last;
+    if (seq) fetch(f);
     if (seq) load_q(bf.b, y, bf.q);
     const bool use = j < n && page >= 0 && page < p.num_pool_pages;
-    if (!seq) bf.nv = use ? 16 : 0;  // the page check, for the later set_seq
-    else if (!use) bf.nv = 0;
+    bf.use = use;
     const int kvh = p.n_hg == 1 ? y : y / p.n_hg;
     const char* kg = reinterpret_cast<const char*>(
         use ? p.kbase + (int64_t)kvh * p.k_head + (int64_t)page * p.k_sa + (int64_t)slot * p.k_sb
@@ -263,40 +270,41 @@ __attribute__((amdgpu_waves_per_eu(stream_min_waves<D, GT>(), 8))) void paged_st
   };
 
   // ---- prologue ----------------------------------------------------------------
-  // The first group's loads need only page ids, which need only the kernel
-  // arguments: they are issued before the sequence table is built (its
-  // barriers wait for LDS only); the table says which sequence a group
-  // belongs to and how many of its tokens are usable.
+  // The first PD groups' page ids, then group 0's K and V, need only the
+  // kernel arguments: they go out before the sequence table is built (its
+  // barriers wait for LDS only).  The table gives the groups' sequences, hence
+  // their q fragments and last-page lengths.
   if (PAIRED && lane == 0)
     __hip_atomic_store(&sm_prog[wave], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-  if (n > 0) {
-    int y0;
-    locate(g0, y0, la_pp, la_slice);
-  }
+  int y0 = 0, pp0 = 0, slice0 = 0;
+  if (n > 0) locate(g0, y0, pp0, slice0);
+  la_y = y0;
+  la_pp = pp0;
+  la_slice = slice0;
 #pragma unroll
-  for (int i = 0; i < PD; ++i) pg[i] = fetch_page();
+  for (int i = 0; i < PD; ++i) {
+    fr[i].page = __builtin_amdgcn_raw_buffer_load_b32(idx_rsrc, (uint32_t)la_pp * 4u, 0, 0);
+    fr[i].y = la_y;
+    fr[i].slot = la_slice * 16;
+    fr[i].b = -1;
+    fr[i].last = 0;
+    fr[i].ll = 0;
+    advance(false);
+  }
   constexpr int ENT = (kStreamMaxBatch + 1 + kSThreads - 1) / kSThreads;  // table entries per thread
-  int tv[ENT], tl[ENT];
+  int tv[ENT];
 #pragma unroll
   for (int j = 0; j < ENT; ++j) {
     const int e = ENT * tid + j;
     tv[j] = e <= p.B ? min(max(p.indptr[e], 0), p.total_pages) : 0;
-    tl[j] = e < p.B ? p.last_len[e] : 0;
   }
   Buf bufs[PD];
-  if (n > 0) {
-    describe_addr(0);
-    issue(0, bufs[0], false, pg[0]);
-  }
+  if (n > 0) issue(0, bufs[0], false, fr[0], false);
   // Sequence table: indptr clamped to [0, total_pages] and made
-  // non-decreasing (a max-scan), last-page lengths clamped to [0, page_size].
+  // non-decreasing (a max-scan).
   {
 #pragma unroll
-    for (int j = 0; j < ENT; ++j) {
-      const int e = ENT * tid + j;
-      if (e < p.B) sm_ll[e] = min(max(tl[j], 0), p.page_size);
-      if (j > 0) tv[j] = max(tv[j], tv[j - 1]);
-    }
+    for (int j = 1; j < ENT; ++j) tv[j] = max(tv[j], tv[j - 1]);
     int incl = tv[ENT - 1];
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) {
@@ -329,16 +337,30 @@ __attribute__((amdgpu_waves_per_eu(stream_min_waves<D, GT>(), 8))) void paged_st
   }
   if (n <= 0) return;  // wave-uniform; no barrier follows
 
-  // Group 0's sequence part and q fragment (loads complete in order, so it is
-  // issued before the other groups), then groups 1 .. PD-1.
-  // (group 0 was issued before its page id could be checked)
-  describe_seq(0);
-  const bool use0 = bufs[0].nv != 0;
-  set_seq(0, bufs[0]);
-  if (!use0) bufs[0].nv = 0;
-  load_q(bufs[0].b, bufs[0].y, bufs[0].q);
+  // Sequences of groups 0 .. PD-1 (their last-page lengths are loaded into
+  // their buffers), then the lookahead from group PD on.  Group 0's q
+  // fragment, group PD's fetch, then groups 1 .. PD-1: each buffer's loads in
+  // the order of the main loop's, so that the compiler's wait counts at the
+  // loop's entry match those of its iterations.
+  la_y = y0;
+  la_pp = pp0;
+  la_slice = slice0;
+  seek(pp0);
 #pragma unroll
-  for (int i = 1; i < PD; ++i) issue(i, bufs[i], true, pg[i]);
+  for (int i = 0; i < PD; ++i) {
+    const bool seq_ok = la_b >= 0 && la_b < p.B;
+    fr[i].b = seq_ok ? la_b : -1;
+    fr[i].last = seq_ok && la_pp == la_end - 1;
+    const int lb = min(max(la_b, 0), p.B - 1);
+    bufs[i].ll = __builtin_amdgcn_raw_buffer_load_b32(ll_rsrc, (uint32_t)lb * 4u, 0, 0);
+    advance(true);
+  }
+  bufs[0].b = fr[0].b;
+  bufs[0].last = fr[0].last;
+  load_q(bufs[0].b, bufs[0].y, bufs[0].q);
+  fetch(fr[0]);
+#pragma unroll
+  for (int i = 1; i < PD; ++i) issue(i, bufs[i], true, fr[i], false);
 
   // ---- state of the unit being streamed ------------------------------------
   float m_run = AKT_SNEG_INF;  // running max of head c16 (log2 units)
@@ -387,8 +409,7 @@ __attribute__((amdgpu_waves_per_eu(stream_min_waves<D, GT>(), 8))) void paged_st
   //   4R .. 4R+3 of dim 16t + c), B = P^T straight from the score lanes
   //   (lane (R, c) holds head c's probabilities of tokens 4R .. 4R+3).
   half_t* const vst = &sm_v[wave][0];
-  auto consume = [&](const Buf& bf) __attribute__((always_inline)) {
-    const int nv = bf.nv;
+  auto consume = [&](const Buf& bf, int nv) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < VTOK; ++i)
 #pragma unroll
@@ -518,7 +539,8 @@ __attribute__((amdgpu_waves_per_eu(stream_min_waves<D, GT>(), 8))) void paged_st
         cur_b = bf.b;
         cur_y = bf.y;
       }
-      if (bf.b >= 0 && bf.nv > 0) consume(bf);
+      const int nv = usable(bf);
+      if (nv > 0) consume(bf, nv);
       balance();
     };
     // Every iteration issues its loads (groups past the range read the q
@@ -527,7 +549,7 @@ __attribute__((amdgpu_waves_per_eu(stream_min_waves<D, GT>(), 8))) void paged_st
 #pragma unroll
       for (int i = 0; i < PD; ++i) {
         if (j + i < n) step(bufs[i]);
-        issue(j + i + PD, bufs[i], true, pg[i]);
+        issue(j + i + PD, bufs[i], true, fr[i], true);
       }
     }
     if (cur_b >= 0) flush();
@@ -543,24 +565,13 @@ __attribute__((amdgpu_waves_per_eu(stream_min_waves<D, GT>(), 8))) void paged_st
   // Every partial store of this wave (device scope) is complete before any
   // count; the merging wave reads the partials with device-scope loads.
   __builtin_amdgcn_s_waitcnt(0);
-  constexpr int NV = GT * D / 4;                 // float4 vectors of a unit's output
-  constexpr int NVL = NV >= 64 ? NV / 64 : 1;    // per lane
-  constexpr int U = NVL >= 16 ? 1 : 16 / NVL;    // partials per round trip
-  auto combine = [](float& M, float& L, float& E, float4_t& A, float m, float l, float e,
-                    float4_t a) __attribute__((always_inline)) {
-    if (m == AKT_SNEG_INF) return;
-    if (m > M) {
-      const float s = fast_exp2(M - m);  // 0 while M = -inf (A, L, E are 0 then)
-      A *= s;
-      L *= s;
-      E *= s;
-      M = m;
-    }
-    const float f = fast_exp2(m - M);
-    A += f * a;
-    L += f * l;
-    E += f * e;
-  };
+  // Merge layout: lane l owns NVL consecutive float4 vectors of the unit's
+  // output (vectors l*NVL .. l*NVL + NVL - 1), all of one head (64 is a
+  // multiple of GT), so it needs one (m, l, e) row per partial; U partials
+  // are loaded per round trip.
+  constexpr int NV = GT * D / 4;               // float4 vectors of a unit's output
+  constexpr int NVL = NV >= 64 ? NV / 64 : 1;  // per lane
+  constexpr int U = 32 / (NVL + 1) > 0 ? 32 / (NVL + 1) : 1;
   // Counts of both partials, issued before either result is awaited.
   int prev_a = 0, prev_b = 0;
   if (lane == 0) {
@@ -569,53 +580,53 @@ __attribute__((amdgpu_waves_per_eu(stream_min_waves<D, GT>(), 8))) void paged_st
   }
   const bool last_a = __builtin_amdgcn_readfirstlane(prev_a) == pa_nc - 1;
   const bool last_b = pb_unit >= 0 && __builtin_amdgcn_readfirstlane(prev_b) == pb_nc - 1;
-  // The wave that counted a unit's last partial resets its counter and merges.
+  // The wave that counted a unit's last partial resets its counter and merges
+  // the unit's partials in wave order.
   auto merge = [&](int unit, int b, int hq0, int nh, int wf, int nc) __attribute__((always_inline)) {
     if (lane == 0) atomicExch(&p.arrive[unit], 0);
-    float M[NVL], L[NVL], E[NVL];
+    const int vec0 = (NV < 64 ? min(lane, NV - 1) : lane * NVL);
+    const int h = (vec0 * 4) / D;
+    const int d0 = vec0 * 4 - h * D;
+    float M = AKT_SNEG_INF, L = 0.f, E = 0.f;
     float4_t Acc[NVL];
 #pragma unroll
-    for (int i = 0; i < NVL; ++i) {
-      M[i] = AKT_SNEG_INF;
-      L[i] = E[i] = 0.f;
-      Acc[i] = float4_t{0.f, 0.f, 0.f, 0.f};
-    }
-    const int vlim = NV < 64 ? NV : 64;
-    const int vl = lane < vlim ? lane : 0;
+    for (int i = 0; i < NVL; ++i) Acc[i] = float4_t{0.f, 0.f, 0.f, 0.f};
     for (int c0 = 0; c0 < nc; c0 += U) {
-      float4_t ml[U][NVL], ov[U][NVL];
+      float4_t ml[U], ov[U][NVL];
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int c = min(c0 + u, nc - 1);
-        const int64_t slot = (int64_t)wf + c + unit;
+        const int64_t ph = ((int64_t)wf + c + unit) * GT + h;
+        ml[u] = as_float4u(ld16_device(p.part_ml, (uint32_t)(ph * 16)));
 #pragma unroll
-        for (int i = 0; i < NVL; ++i) {
-          const int vec = vl + 64 * i;
-          const int h = (vec * 4) / D;
-          const int64_t ph = slot * GT + h;
-          ml[u][i] = as_float4u(ld16_device(p.part_ml, (uint32_t)(ph * 16)));
-          ov[u][i] = as_float4u(ld16_device(p.part_o, (uint32_t)((ph * D + vec * 4 - h * D) * 4)));
-        }
+        for (int i = 0; i < NVL; ++i)
+          ov[u][i] = as_float4u(ld16_device(p.part_o, (uint32_t)((ph * D + d0 + 4 * i) * 4)));
       }
 #pragma unroll
-      for (int u = 0; u < U; ++u)
-        if (c0 + u < nc)
+      for (int u = 0; u < U; ++u) {
+        const float m = ml[u][0];
+        if (c0 + u >= nc || m == AKT_SNEG_INF) continue;
+        if (m > M) {
+          const float s = fast_exp2(M - m);  // 0 while M = -inf (Acc, L, E are 0 then)
 #pragma unroll
-          for (int i = 0; i < NVL; ++i)
-            combine(M[i], L[i], E[i], Acc[i], ml[u][i][0], ml[u][i][1], ml[u][i][2], ov[u][i]);
+          for (int i = 0; i < NVL; ++i) Acc[i] *= s;
+          L *= s;
+          E *= s;
+          M = m;
+        }
+        const float f = fast_exp2(m - M);
+#pragma unroll
+        for (int i = 0; i < NVL; ++i) Acc[i] += f * ov[u][i];
+        L += f * ml[u][1];
+        E += f * ml[u][2];
+      }
     }
-    if (lane < vlim) {
+    if ((NV >= 64 || lane < NV) && h < nh) {
+      const int64_t row = (int64_t)b * p.Hq + hq0 + h;
+      const float inv = L > 0.f ? 1.0f / L : 0.f;
 #pragma unroll
-      for (int i = 0; i < NVL; ++i) {
-        const int vec = lane + 64 * i;
-        const int h = (vec * 4) / D;
-        const int d0 = vec * 4 - h * D;
-        if (h < nh) {
-          const int64_t row = (int64_t)b * p.Hq + hq0 + h;
-          store_o4(row, d0, Acc[i], L[i] > 0.f ? 1.0f / L[i] : 0.f);
-          if (d0 == 0) store_lse(row, M[i], E[i]);
-        }
-      }
+      for (int i = 0; i < NVL; ++i) store_o4(row, d0 + 4 * i, Acc[i], inv);
+      if (d0 == 0) store_lse(row, M, E);
     }
   };
   if (last_a) merge(pa_unit, pa_b, pa_hq0, pa_nh, pa_wf, pa_nc);
