@@ -195,18 +195,22 @@ __attribute__((amdgpu_waves_per_eu(stream_min_waves<D, GT>(), 8))) void paged_st
     uint4_t k[KS];
     uint4_t v[VTOK][VLD];
     half8_t q[KS];  // the query fragment of the group's unit
-    int ll;         // the sequence's last-page length (loaded)
     // wave-uniform: sequence (-1: none or a dummy), head group, first row of
-    // the slice, whether the page is the sequence's last, valid page id
-    int b, y, slot, last, use;
+    // the slice, whether the page is the sequence's last, valid page id,
+    // usable tokens
+    int b, y, slot, last, use, nv;
   };
-  // Usable tokens of a buffer's group: 16, or on the sequence's last page the
-  // rows below its length (clamped to [0, page_size]), 0 for invalid pages.
-  auto usable = [&](const Buf& bf) __attribute__((always_inline)) -> int {
-    if (!bf.use || bf.b < 0) return 0;
-    if (!bf.last) return 16;
-    const int ll = min(max(uniform(bf.ll), 0), p.page_size);
-    return min(max(ll - bf.slot, 0), 16);
+  // Usable tokens of a buffer's group given its sequence's last-page length
+  // ll (a loaded register): 16, or on the sequence's last page the rows below
+  // ll (clamped to [0, page_size]), 0 for invalid pages.  The length is read
+  // into a scalar here, when the group is issued (its load, PD groups back,
+  // is complete then), so that no vector register holding a loaded value is
+  // carried from one group to the next: the compiler may copy such a register
+  // at the loop's head, and would wait there for the load that last wrote it.
+  auto set_usable = [&](Buf& bf, int ll_reg) __attribute__((always_inline)) {
+    const int ll = min(max(uniform(ll_reg), 0), p.page_size);
+    const int tail = min(max(ll - bf.slot, 0), 16);
+    bf.nv = (!bf.use || bf.b < 0) ? 0 : (bf.last ? tail : 16);
   };
 
   // Query fragment of unit (b, y) (MFMA B operand): head hq0 + c16, dims
@@ -229,8 +233,8 @@ __attribute__((amdgpu_waves_per_eu(stream_min_waves<D, GT>(), 8))) void paged_st
 
   // Issues group j of this wave from its fetch record f (j >= n: a dummy
   // group that reads the q row), then fetches group j + PD into f.
-  // `take_ll`: f's last-page length goes to the buffer (the prologue loads
-  // it into the buffer itself).  Rows of a
+  // `take_ll`: the usable tokens are set from f's last-page length (the
+  // prologue sets them itself).  Rows of a
   // valid page are loaded whole; tokens past the usable prefix are masked when
   // consumed.  `seq`: the sequence is known (the table exists), so the unit's
   // q fragment is loaded with the group.  Every call issues the same loads
@@ -242,15 +246,15 @@ __attribute__((amdgpu_waves_per_eu(stream_min_waves<D, GT>(), 8))) void paged_st
                    __attribute__((always_inline)) {
     const int page = uniform(f.page);
     const int y = f.y, slot = f.slot;
-    if (take_ll) bf.ll = f.ll;
     bf.b = j < n ? f.b : -1;
     bf.y = y;
     bf.slot = slot;
     bf.last = f.last;
-    if (seq) fetch(f);
-    if (seq) load_q(bf.b, y, bf.q);
     const bool use = j < n && page >= 0 && page < p.num_pool_pages;
     bf.use = use;
+    if (take_ll) set_usable(bf, f.ll);
+    if (seq) fetch(f);
+    if (seq) load_q(bf.b, y, bf.q);
     const int kvh = p.n_hg == 1 ? y : y / p.n_hg;
     const char* kg = reinterpret_cast<const char*>(
         use ? p.kbase + (int64_t)kvh * p.k_head + (int64_t)page * p.k_sa + (int64_t)slot * p.k_sb
@@ -338,7 +342,7 @@ __attribute__((amdgpu_waves_per_eu(stream_min_waves<D, GT>(), 8))) void paged_st
   if (n <= 0) return;  // wave-uniform; no barrier follows
 
   // Sequences of groups 0 .. PD-1 (their last-page lengths are loaded into
-  // their buffers), then the lookahead from group PD on.  Group 0's q
+  // pll), then the lookahead from group PD on.  Group 0's q
   // fragment, group PD's fetch, then groups 1 .. PD-1: each buffer's loads in
   // the order of the main loop's, so that the compiler's wait counts at the
   // loop's entry match those of its iterations.
@@ -346,13 +350,14 @@ __attribute__((amdgpu_waves_per_eu(stream_min_waves<D, GT>(), 8))) void paged_st
   la_pp = pp0;
   la_slice = slice0;
   seek(pp0);
+  int pll[PD];
 #pragma unroll
   for (int i = 0; i < PD; ++i) {
     const bool seq_ok = la_b >= 0 && la_b < p.B;
     fr[i].b = seq_ok ? la_b : -1;
     fr[i].last = seq_ok && la_pp == la_end - 1;
     const int lb = min(max(la_b, 0), p.B - 1);
-    bufs[i].ll = __builtin_amdgcn_raw_buffer_load_b32(ll_rsrc, (uint32_t)lb * 4u, 0, 0);
+    pll[i] = __builtin_amdgcn_raw_buffer_load_b32(ll_rsrc, (uint32_t)lb * 4u, 0, 0);
     advance(true);
   }
   bufs[0].b = fr[0].b;
@@ -361,6 +366,8 @@ __attribute__((amdgpu_waves_per_eu(stream_min_waves<D, GT>(), 8))) void paged_st
   fetch(fr[0]);
 #pragma unroll
   for (int i = 1; i < PD; ++i) issue(i, bufs[i], true, fr[i], false);
+#pragma unroll
+  for (int i = 0; i < PD; ++i) set_usable(bufs[i], pll[i]);
 
   // ---- state of the unit being streamed ------------------------------------
   float m_run = AKT_SNEG_INF;  // running max of head c16 (log2 units)
@@ -539,8 +546,7 @@ __attribute__((amdgpu_waves_per_eu(stream_min_waves<D, GT>(), 8))) void paged_st
         cur_b = bf.b;
         cur_y = bf.y;
       }
-      const int nv = usable(bf);
-      if (nv > 0) consume(bf, nv);
+      if (bf.nv > 0) consume(bf, bf.nv);
       balance();
     };
     // Every iteration issues its loads (groups past the range read the q
