@@ -315,9 +315,14 @@ __attribute__((amdgpu_waves_per_eu(split_min_waves<D, GT>(), 8))) void split_ker
       w.pstart = p.indptr[w.b];
       w.np = p.indptr[w.b + 1] - w.pstart;
     } else if constexpr (SPARSE) {
+      // Block x is split c = x / rows of row u = x % rows: consecutive blocks,
+      // which the dispatcher deals to the XCDs in turn, are different rows,
+      // so that the splits of one row (and the short last splits) spread
+      // over the XCDs.
       const int x = blockIdx.x;
-      const int u = x / p.n_split;
-      const int c = x - u * p.n_split;
+      const int rows = (int)gridDim.x / p.n_split;
+      const int c = x / rows;
+      const int u = x - c * rows;
       w.b = u / p.Hq;
       w.hq0 = u - w.b * p.Hq;
       w.kvh = w.hq0 / p.G;
@@ -337,12 +342,12 @@ __attribute__((amdgpu_waves_per_eu(split_min_waves<D, GT>(), 8))) void split_ker
         // with the harness's -1 padding that slot names the last row.
         if constexpr (MODE == kModeSparseDense) n = max(n, min(1, p.l_max));
       }
-      // Split c covers [c*per, min(n, (c+1)*per)); per is a multiple of 64 so
+      // Split c covers [c*per, min(n, (c+1)*per)); per is a multiple of 16 so
       // every split starts on a 16-token group and splits never share a group.
-      const int per = ((n + p.n_split - 1) / p.n_split + 63) & ~63;
+      const int per = ((n + p.n_split - 1) / p.n_split + 15) & ~15;
       w.t0 = c * per;
       w.t1 = max(w.t0, min(n, w.t0 + per));
-      w.pidx = x;
+      w.pidx = (int64_t)u * p.n_split + c;
       w.direct = (p.n_split == 1);
       w.nch = p.n_split;
       w.unit = u;
