@@ -277,12 +277,14 @@ def _ceilings(cfg, sets, args):
         "ceiling_gather_config3": _leg(
             "gather ceiling", [lambda p=p: gather(p) for p in sets], gather_bytes, "GB/s",
             "paged_gather_kernel<4>", args,
+            traffic=_traffic("legs_hbm_traffic.md", "ceiling_gather_config3"),
             note=f"reads every (page, kv head) K and V block of config 3's page table "
                  f"({total} pages x {Hkv} kv heads x 8 KB) and nothing else; {len(sets)} input "
                  "sets rotated"),
         "ceiling_stream_read_config3": _leg(
             "stream ceiling", [lambda p=p: stream(p) for p in sets], pool_bytes, "GB/s",
             "stream_read_kernel", args,
+            traffic=_traffic("legs_hbm_traffic.md", "ceiling_stream_read_config3"),
             note=f"reads each {pool_bytes} B pool in order; {len(sets)} pools rotated"),
     }
     return out
