@@ -25,7 +25,8 @@ dense fp16); roofline.traffic is the HBM bytes per launch from the committed
 rocprofv3 counter summary in profiles/, where one exists.  Legs whose working
 set is under twice the 256 MB Infinity Cache rotate over copies of their
 inputs.  cpu_baseline is the repository's CPU restatement of the reference's
-naive path (oracle/, fp32 torch/numpy) timed on a bounded sample on this host.
+naive path in its fp16 op order (oracle/ref_order.py) timed on a bounded
+sample on this host.
 
 Usage: python bench.py [--steps K] [--warmup W] [--gpus 1]
 Prints one JSON line.

@@ -181,6 +181,12 @@ int akt_decode_fwd(const void* q, const void* k, const void* v, void* o, float* 
  *   has no pages; last_page_len is clamped to [0, page_size]).  Page ids
  *   outside [0, num_pool_pages) are skipped.
  *   o: contiguous [batch, num_q_heads, head_dim]; lse optional [batch, num_q_heads].
+ *   chunk_tokens 0 (automatic) runs the stream-K kernel when batch <= 1024
+ *   and page_size is a multiple of 16: every wave of the launch takes a fixed
+ *   range of 16-token groups, and its workspace holds one partial per wave
+ *   the device keeps resident plus one per (sequence, head group), so the
+ *   workspace size depends on the current device.  Otherwise, and for the
+ *   explicit lengths 128, 256, 512 or 640, the chunked split kernel runs.
  */
 size_t akt_decode_paged_workspace_size(int64_t batch, int64_t num_q_heads, int64_t num_kv_heads,
                                        int64_t head_dim, int64_t page_size, int64_t total_pages,
