@@ -319,6 +319,30 @@ def test_paged_batch_past_the_lds_chunk_table(dev, page):
     assert torch.isinf(lse.cpu()[~nonempty]).all()
 
 
+@pytest.mark.parametrize("B", [1, 63, 64, 200, 1024])
+def test_paged_batches_up_to_the_lds_sequence_table(dev, B):
+    """The automatic path builds every workgroup's sequence table in LDS, up to
+    1024 sequences: batches from one sequence to that limit, with empty
+    sequences and clamped last-page lengths, match the oracle (O and LSE)."""
+    g = torch.Generator().manual_seed(70 + B)
+    Hq, Hkv, D, page = 8, 2, 128, 16
+    lens = torch.randint(1, 300, (B,), generator=g).tolist()
+    for b in {0, B // 2, B - 1} if B > 2 else set():
+        lens[b] = 0
+    indptr, indices, last, P = syn.block_table(g, lens, page, extra_pages=3)
+    if B > 1:
+        last[1] = 40  # clamps to the page size
+    pool = torch.randn(P, 2, Hkv, page, D, generator=g).half()
+    q = torch.randn(B, Hq, 1, D, generator=g).half()
+    o, lse = pg.flash_attention_decode_paged(q.to(dev), pool.to(dev), indptr.to(dev),
+                                             indices.to(dev), last.to(dev), return_lse=True)
+    ro, rl = naive.naive_paged_attention(q, pool, indptr, indices, last)
+    nonempty = (indptr[1:] - indptr[:-1]) > 0
+    assert_close(o, ro, what=f"paged B={B}")
+    assert_close(lse, rl, atol=1e-4, what=f"paged lse B={B}", mask=nonempty)
+    assert torch.isinf(lse.cpu()[~nonempty]).all()
+
+
 def test_paged_merges_are_coherent_across_launches(dev):
     """The last workgroup of a unit merges partials other workgroups (on any XCD)
     stored in the same launch.  Alternating two inputs over one workspace, every
