@@ -343,6 +343,24 @@ def test_paged_batches_up_to_the_lds_sequence_table(dev, B):
     assert torch.isinf(lse.cpu()[~nonempty]).all()
 
 
+@pytest.mark.parametrize("G,D", [(1, 128), (2, 64), (3, 128), (8, 256), (16, 128), (32, 64)])
+def test_paged_automatic_path_every_head_group_width(dev, G, D):
+    """Every heads-per-unit instance of the automatic path (GT = 1, 2, 4, 8,
+    16; G = 3 leaves a unit's last column empty, G = 32 at D = 64 takes two
+    head groups of 16 per kv head) against the oracle, O and LSE."""
+    g = torch.Generator().manual_seed(90 + G + D)
+    Hkv, page = 2, 32
+    lens = torch.randint(1, 900, (6,), generator=g).tolist()
+    indptr, indices, last, P = syn.block_table(g, lens, page, extra_pages=2)
+    pool = torch.randn(P, 2, Hkv, page, D, generator=g).half()
+    q = torch.randn(len(lens), Hkv * G, 1, D, generator=g).half()
+    o, lse = pg.flash_attention_decode_paged(q.to(dev), pool.to(dev), indptr.to(dev),
+                                             indices.to(dev), last.to(dev), return_lse=True)
+    ro, rl = naive.naive_paged_attention(q, pool, indptr, indices, last)
+    assert_close(o, ro, what=f"paged G={G} D={D}")
+    assert_close(lse, rl, atol=1e-4, what=f"paged lse G={G} D={D}")
+
+
 def test_paged_merges_are_coherent_across_launches(dev):
     """The last workgroup of a unit merges partials other workgroups (on any XCD)
     stored in the same launch.  Alternating two inputs over one workspace, every
